@@ -1,0 +1,170 @@
+/*
+ * liblaya_hip: C ABI of the MI355X (gfx950) encoder forward path.
+ *
+ * This is the drop-in boundary under laya-cuda's Python runtime.  The reference's Runtime
+ * (laya_cuda/runtime.py:136-197) owns a CuPy memory pool, one stream, the resident weights and an
+ * LRU of shape slots, each with a CUDA graph; Ops (laya_cuda/ops.py:19-71) owns NVRTC kernels and
+ * cuBLAS.  Here one opaque engine handle owns all of that natively: an HBM arena per slot, one
+ * non-blocking HIP stream, resident weights, and one hipGraph per shape slot.
+ *
+ * Conventions: every entry point returns 0 (LAYA_OK) or a LAYA_E* status; the message of the
+ * last failure is laya_last_error(handle) (handle may be NULL for failures that have none).
+ * Pointers named host_* are host memory; every other buffer pointer of the laya_op_* entry
+ * points is device memory.  `stream` is a hipStream_t (NULL = the null stream).  A handle is
+ * single-threaded: callers serialise access (as the reference's Engine and BatchEngine do).
+ */
+#ifndef LAYA_HIP_H
+#define LAYA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LAYA_ABI_VERSION 1
+
+enum {
+  LAYA_OK = 0,
+  LAYA_EINVAL = 1,   /* bad argument, name, shape or configuration */
+  LAYA_EDEVICE = 2,  /* HIP runtime failure */
+  LAYA_ENOMEM = 3,   /* device or pinned allocation failed */
+  LAYA_ESTATE = 4    /* call out of order (e.g. predict before finalize) */
+};
+
+/* Element types of host weights and of the 16-bit MFMA operand type. */
+enum { LAYA_F32 = 0, LAYA_F16 = 1, LAYA_BF16 = 2 };
+
+/* Encoder variants (the reference's executor is pre-LN/RoPE/GeGLU, laya_cuda/laya.py:59-79). */
+enum { LAYA_NORM_POST = 0, LAYA_NORM_PRE = 1 };
+enum { LAYA_POS_LEARNED = 0, LAYA_POS_ROPE = 1 };
+enum { LAYA_FFN_GELU = 0, LAYA_FFN_GEGLU = 1 };
+
+/* Model configuration: the fields the reference's adapter exposes to Runtime
+ * (width, heads, layers, intermediate, eps, max_len, n_act, ...; laya_cuda/laya.py:61-81). */
+typedef struct LayaConfig {
+  int32_t width;          /* d_model; heads * 64 */
+  int32_t heads;
+  int32_t layers;
+  int32_t intermediate;   /* FFN width f */
+  int32_t vocab;
+  int32_t max_positions;  /* learned position rows */
+  int32_t type_vocab;     /* token-type rows (row 0 is added) */
+  int32_t norm_order;     /* LAYA_NORM_* */
+  int32_t pos_kind;       /* LAYA_POS_* */
+  int32_t ffn_kind;       /* LAYA_FFN_* */
+  int32_t bias;           /* encoder linear layers carry biases */
+  float eps;              /* encoder LayerNorm epsilon */
+  int32_t window;         /* local attention half-window, -1 = global */
+  int32_t global_every;
+  int32_t head_layers;    /* decision-head transformer layers */
+  int32_t n_act;          /* act-head outputs */
+  int32_t act_hidden;     /* act-head hidden width (256 in Laya) */
+  int32_t max_len;        /* longest sequence, tokens */
+  int32_t mfma_dtype;     /* LAYA_BF16 or LAYA_F16: resident matrices and MFMA operands */
+} LayaConfig;
+
+/* Shape class of one predict: the reference's slot key (laya_cuda/runtime.py:20-25). */
+typedef struct LayaShape {
+  int32_t rows;     /* packed token rows m (multiple of 16) */
+  int32_t batch;    /* question capacity b (also the sequence capacity) */
+  int32_t options;  /* option capacity k per question */
+} LayaShape;
+
+typedef struct LayaMetrics {
+  float gpu_ms;            /* stream time of the forward (graph replay or eager), events */
+  int32_t cache_miss;      /* the slot was created by this call */
+  int32_t graph_capture;   /* the slot's graph was captured by this call */
+  int32_t graph_replay;    /* the forward ran as a graph replay */
+  int64_t owned_gpu_bytes; /* weights + slot arenas */
+} LayaMetrics;
+
+/*
+ * Packed int32 input block of a predict, laid out for shape (m, b, k):
+ *   meta[4]          n_seq, n_questions, 0, 0
+ *   ids[m] positions[m] rows[m] kinds[m]            per packed token (runtime.py:35-36)
+ *   starts[b] lengths[b]                            per sequence
+ *   counts[b] qkind[b]                              per question
+ *   indices[b*(k+1)]                                per question: CLS row, then option rows,
+ *                                                   absolute packed rows (runtime.py:63-66)
+ * laya_packed_ints(shape) gives its length.  Sequences start at multiples of 16 rows; rows of
+ * no sequence carry rows[i] = -1.
+ */
+int64_t laya_packed_ints(const LayaShape* shape);
+
+/* Runtime(adapter, device, max_cached_shapes) construction (runtime.py:137-146). */
+int laya_create(const LayaConfig* cfg, int device, int max_slots, void** handle);
+
+/* Upload one named checkpoint tensor (runtime.py:147-158): the name set and shapes are those of
+ * the adapter's weight_shapes(); matrices feeding MFMA become resident in cfg->mfma_dtype, all
+ * other tensors in fp32.  host_dtype is LAYA_F32/F16/BF16, shape has ndim entries. */
+int laya_load_weight(void* handle, const char* name, const void* host_data, int host_dtype,
+                     const int64_t* shape, int ndim);
+
+/* Checks that every tensor is present and resolves the layer tables.  Required before predict. */
+int laya_finalize(void* handle);
+
+/* Runtime.predict / Slot.run (runtime.py:115-133, 171-186): find or create the shape slot (LRU
+ * eviction at max_slots), upload the packed block, capture the slot's graph on first use when
+ * capture != 0, replay (or run eagerly), and copy back host_logits [b][k] (option slots 1..k,
+ * laya.py:208) and host_acts [b][n_act]. */
+int laya_predict(void* handle, const int32_t* host_packed, const LayaShape* shape, int capture,
+                 float* host_logits, float* host_acts, LayaMetrics* metrics);
+
+/* Read a resident tensor back as fp32 (runtime.weights[name], tests/test_custom_models.py:46). */
+int laya_read_weight(void* handle, const char* name, float* host_out, int64_t count);
+int64_t laya_used_bytes(void* handle);   /* weights + slots: CuPy pool used_bytes() */
+int laya_slot_count(void* handle);       /* len(runtime.slots) */
+int laya_destroy(void* handle);          /* Runtime.close (runtime.py:188-197) */
+const char* laya_last_error(void* handle);
+int laya_abi_version(void);
+
+/* ------------------------------------------------------------------------------------------
+ * Kernel-level entry points: the Ops surface the reference's kernel tests drive
+ * (laya_cuda/ops.py:50-66; tests/test_gpu.py, tests/test_attention.py).
+ * ------------------------------------------------------------------------------------------ */
+
+/* Attention work list for packed sequences: tiles of up to `block` query rows of one sequence,
+ * plus zero-tiles for rows of no sequence; writes (row0,row1,seq) triples, returns the count
+ * (or -1 if max_tiles is too small).  Host-only. */
+int laya_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_seq, int m, int block,
+                         int32_t* tiles, int max_tiles);
+int laya_attention_block(int waves);
+
+/* embed (kernels.cu:16-19) fused with the embeddings norm (runtime.py:93-95):
+ * v = table[ids] (+ pos_table[positions]) (+ type_row); LayerNorm if gamma; writes out32 and/or
+ * out16 (dtype16 = LAYA_BF16/F16). */
+int laya_op_embed(const int32_t* ids, const int32_t* positions, const float* table,
+                  const float* pos_table, const float* type_row, const float* gamma,
+                  const float* beta, float eps, float* out32, void* out16, int dtype16, int rows,
+                  int width, int vocab, int n_positions, void* stream);
+
+/* layer_norm (kernels.cu:20-49): v = residual + (sum of `splits` branch partials + bias);
+ * sum_out = v; LayerNorm if gamma; out32/out16 = result.  out32 may alias residual. */
+int laya_op_norm(float* residual, const float* branch, int splits, int64_t part_stride,
+                 const float* bias, const float* gamma, const float* beta, float eps,
+                 float* sum_out, float* out32, void* out16, int dtype16, int rows, int width,
+                 void* stream);
+
+/* Ops.linear (ops.py:58-66): out[M][N] = x[M][K] w[N][K]^T (+ bias).  kind 0: fp32 out
+ * (split-K partials at out + z*M*N when splits > 1, bias then must be NULL), 1: 16-bit out,
+ * 2: 16-bit GELU out.  tile < 0 lets the planner choose tile and splits (splits ignored). */
+int laya_op_linear(const void* x, const void* w, const float* bias, void* out, int kind,
+                   int dtype16, int M, int N, int K, int splits, int tile, void* stream);
+
+/* QKV projection with the head-major epilogue that replaces `layout` (kernels.cu:68-82):
+ * q, k [heads][M][64], vt [heads][64][M]. */
+int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* k, void* vt,
+                int dtype16, int M, int width, int tile, void* stream);
+
+/* attention (kernels.cu:90-154, window -1) over a tile list from laya_attention_tiles. */
+int laya_op_attention(const void* q, const void* k, const void* vt, void* out,
+                      const int32_t* tiles, const int32_t* n_tiles, const int32_t* starts,
+                      const int32_t* lengths, int m, int heads, int max_tiles, int waves,
+                      int dtype16, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LAYA_HIP_H */

@@ -1,0 +1,275 @@
+// MFMA-tiled GEMM for the encoder projections: out = A * B^T (+ bias) with fused epilogues.
+//
+// Both operands are K-contiguous ("NT": activations [M][K], weights [N][K], the reference's
+// cublasGemmEx orientation at laya_cuda/ops.py:63-64), which is exactly what the gfx950
+// v_mfma_f32_32x32x16_{bf16,f16} operands want: each lane feeds 8 consecutive k of one row.
+//
+// Workgroup: 256 threads = 4 waves on a WM x WN grid; each wave owns (BM/WM) x (BN/WN) made of
+// 32x32 MFMA tiles.  K advances in 64-wide slabs staged through LDS, double-buffered: the next
+// slab's global loads are in flight (registers) while the current slab feeds the MFMAs, then
+// land in the other LDS buffer; one barrier per slab.  LDS rows are 128 B (64 x 16-bit) with the
+// 16-byte chunk index XOR-swizzled by (row & 7), so the 32 lanes reading one k-chunk of 32
+// consecutive rows hit distinct banks.
+//
+// Epilogues (all fp32 until the single final rounding, bias added before it as in
+// laya_cuda/kernels.cu:50-55):
+//   F32  - fp32 partial of split z to out + z*split_stride (split-K reduction happens in the
+//          residual+LayerNorm kernel that consumes it);
+//   HALF - + bias, rounded to 16-bit;
+//   GELU - + bias, exact-erf GELU, rounded to 16-bit (FFN up);
+//   QKV  - + bias, rounded, written head-major: Q,K [h][M][64] and V transposed [h][64][M]
+//          (replaces the reference's separate `layout` pass, kernels.cu:68-82).
+#include "kernels.hpp"
+
+namespace laya {
+
+namespace {
+
+constexpr int BK = 64;
+
+template <typename T, int BM, int BN, int WM, int WN, Epi E>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
+  static_assert(WM * WN == 4, "four waves per workgroup");
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "32x32 MFMA tiles");
+  constexpr int ACH = BM * 8 / 256;  // 16-byte chunks per thread per slab
+  constexpr int BCH = BN * 8 / 256;
+  typedef typename Vec8<T>::type T8;
+
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* sA = reinterpret_cast<T*>(smem_raw);
+  T* sB = sA + 2 * BM * BK;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM, z = blockIdx.z;
+
+  const T* A = static_cast<const T*>(a.a);
+  const T* B = static_cast<const T*>(a.b);
+  const int nk = a.K / BK;
+  const int per = (nk + a.splits - 1) / a.splits;
+  const int kb = z * per, ke = min(nk, kb + per);
+
+  i32x4 ra[ACH], rb[BCH];
+  auto gload = [&](int kt) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      const int g = min(m0 + row, a.M - 1);
+      ra[i] = *reinterpret_cast<const i32x4*>(A + static_cast<size_t>(g) * a.lda + k0 + ch * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      rb[i] = *reinterpret_cast<const i32x4*>(B + static_cast<size_t>(n0 + row) * a.ldb + k0 + ch * 8);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      *reinterpret_cast<i32x4*>(sA + buf * BM * BK + row * BK + ((ch ^ (row & 7)) << 3)) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      *reinterpret_cast<i32x4*>(sB + buf * BN * BK + row * BK + ((ch ^ (row & 7)) << 3)) = rb[i];
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int lrow = lane & 31, kg = lane >> 5;
+  if (kb < ke) {
+    gload(kb);
+    lstore(0);
+    __syncthreads();
+    for (int kt = kb; kt < ke; ++kt) {
+      const int cur = (kt - kb) & 1;
+      if (kt + 1 < ke) gload(kt + 1);
+      const T* cA = sA + cur * BM * BK;
+      const T* cB = sB + cur * BN * BK;
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; ++kk) {
+        const int ch = kk * 2 + kg;
+        T8 af[TM], bfr[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int r = wm0 + i * 32 + lrow;
+          af[i] = *reinterpret_cast<const T8*>(cA + r * BK + ((ch ^ (r & 7)) << 3));
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int r = wn0 + j * 32 + lrow;
+          bfr[j] = *reinterpret_cast<const T8*>(cB + r * BK + ((ch ^ (r & 7)) << 3));
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(af[i], bfr[j], acc[i][j]);
+      }
+      if (kt + 1 < ke) lstore(cur ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // Epilogue.  Element r of lane l in a 32x32 tile is row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn0 + j * 32 + lrow;
+      const float bias = (E != Epi::F32 || a.splits == 1) && a.bias ? a.bias[col] : 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * kg + (r & 3);
+        if (row >= a.M) continue;
+        const float v = acc[i][j][r] + bias;
+        if constexpr (E == Epi::F32) {
+          static_cast<float*>(a.out)[z * a.split_stride + static_cast<long long>(row) * a.ldo + col] = v;
+        } else if constexpr (E == Epi::HALF) {
+          static_cast<T*>(a.out)[static_cast<long long>(row) * a.ldo + col] = to_half<T>(v);
+        } else if constexpr (E == Epi::GELU) {
+          static_cast<T*>(a.out)[static_cast<long long>(row) * a.ldo + col] = to_half<T>(gelu(v));
+        } else {
+          const int part = col / a.width, hn = col - part * a.width, head = hn >> 6, dim = hn & 63;
+          const T h = to_half<T>(v);
+          if (part == 0) {
+            static_cast<T*>(a.q)[(static_cast<size_t>(head) * a.M + row) * 64 + dim] = h;
+          } else if (part == 1) {
+            static_cast<T*>(a.k)[(static_cast<size_t>(head) * a.M + row) * 64 + dim] = h;
+          } else {
+            static_cast<T*>(a.vt)[(static_cast<size_t>(head) * 64 + dim) * a.M + row] = h;
+          }
+        }
+      }
+    }
+  }
+}
+
+struct TileDef {
+  int bm, bn, wm, wn;
+};
+// Tile menu; the planner picks per problem.  Ids are part of the op-level ABI (tests sweep them).
+constexpr TileDef kTiles[] = {
+    {256, 256, 2, 2},  // 0: wave 128x128, large M (batched)
+    {256, 128, 2, 2},  // 1: wave 128x64
+    {128, 128, 2, 2},  // 2: wave 64x64
+    {128, 64, 2, 2},   // 3: wave 64x32
+    {64, 128, 2, 2},   // 4: wave 32x64
+    {64, 64, 2, 2},    // 5: wave 32x32, small M (batch-1 latency)
+    {32, 128, 1, 4},   // 6: wave 32x32, very small M
+};
+constexpr int kTileCount = sizeof(kTiles) / sizeof(kTiles[0]);
+
+constexpr size_t lds_bytes(int bm, int bn) { return static_cast<size_t>(2) * (bm + bn) * BK * 2; }
+
+template <typename T, Epi E>
+hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
+  const TileDef& d = kTiles[tile];
+  const dim3 grid(a.N / d.bn, (a.M + d.bm - 1) / d.bm, a.splits), block(256);
+  const size_t lds = lds_bytes(d.bm, d.bn);
+  switch (tile) {
+#define LAYA_TILE(ID, BM_, BN_, WM_, WN_) \
+  case ID: hipLaunchKernelGGL((gemm_kernel<T, BM_, BN_, WM_, WN_, E>), grid, block, lds, stream, a); break;
+    LAYA_TILE(0, 256, 256, 2, 2)
+    LAYA_TILE(1, 256, 128, 2, 2)
+    LAYA_TILE(2, 128, 128, 2, 2)
+    LAYA_TILE(3, 128, 64, 2, 2)
+    LAYA_TILE(4, 64, 128, 2, 2)
+    LAYA_TILE(5, 64, 64, 2, 2)
+    LAYA_TILE(6, 32, 128, 1, 4)
+#undef LAYA_TILE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <typename T, Epi E>
+hipError_t set_lds_attr() {
+  hipError_t e = hipSuccess;
+#define LAYA_ATTR(BM_, BN_, WM_, WN_)                                                              \
+  if (e == hipSuccess)                                                                           \
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<T, BM_, BN_, WM_, WN_, E>), \
+                            hipFuncAttributeMaxDynamicSharedMemorySize,                            \
+                            static_cast<int>(lds_bytes(BM_, BN_)));
+  LAYA_ATTR(256, 256, 2, 2)
+  LAYA_ATTR(256, 128, 2, 2)
+  LAYA_ATTR(128, 128, 2, 2)
+#undef LAYA_ATTR
+  return e;
+}
+
+template <typename T>
+hipError_t set_lds_all() {
+  hipError_t e = set_lds_attr<T, Epi::F32>();
+  if (e == hipSuccess) e = set_lds_attr<T, Epi::HALF>();
+  if (e == hipSuccess) e = set_lds_attr<T, Epi::GELU>();
+  if (e == hipSuccess) e = set_lds_attr<T, Epi::QKV>();
+  return e;
+}
+
+}  // namespace
+
+int gemm_tile_count() { return kTileCount; }
+GemmTile gemm_tile(int id) { return GemmTile{kTiles[id].bm, kTiles[id].bn}; }
+
+hipError_t gemm_prepare() {
+  hipError_t e = set_lds_all<bf16>();
+  if (e == hipSuccess) e = set_lds_all<f16>();
+  return e;
+}
+
+void gemm_plan(int M, int N, int K, Epi epi, int cus, int* tile, int* splits) {
+  // Largest tile that still gives every CU a workgroup; small problems fall back to small tiles
+  // and, for the fp32 (split-K capable) epilogue, to K splits until the grid covers the chip.
+  const int order[] = {0, 1, 2, 3, 4, 5, 6};
+  int best = 5, best_split = 1;
+  for (int id : order) {
+    const TileDef& d = kTiles[id];
+    if (N % d.bn) continue;
+    const long long wgs = static_cast<long long>((M + d.bm - 1) / d.bm) * (N / d.bn);
+    const long long waste_rows = static_cast<long long>((M + d.bm - 1) / d.bm) * d.bm - M;
+    if (waste_rows * 4 > M) continue;  // more than 25% padding rows
+    if (wgs >= cus) {
+      best = id;
+      best_split = 1;
+      break;
+    }
+    best = id;
+  }
+  const TileDef& d = kTiles[best];
+  const long long wgs = static_cast<long long>((M + d.bm - 1) / d.bm) * (N / d.bn);
+  if (epi == Epi::F32) {
+    const int nk = K / BK;
+    while (wgs * best_split < cus && best_split * 2 <= nk / 4 && best_split < 8) best_split *= 2;
+  }
+  *tile = best;
+  *splits = best_split;
+}
+
+hipError_t launch_gemm(const GemmArgs& a, Epi epi, DType t, int tile, hipStream_t stream) {
+  if (tile < 0 || tile >= kTileCount) return hipErrorInvalidValue;
+  if (a.M <= 0) return hipSuccess;
+  if (a.K % BK || a.N % kTiles[tile].bn || a.splits < 1) return hipErrorInvalidValue;
+  if (epi != Epi::F32 && a.splits != 1) return hipErrorInvalidValue;
+  if (epi == Epi::F32 && a.splits != 1 && a.bias) return hipErrorInvalidValue;  // bias joins the sum later
+  const bool h = t == DType::F16;
+  switch (epi) {
+    case Epi::F32: return h ? launch_t<f16, Epi::F32>(a, tile, stream) : launch_t<bf16, Epi::F32>(a, tile, stream);
+    case Epi::HALF: return h ? launch_t<f16, Epi::HALF>(a, tile, stream) : launch_t<bf16, Epi::HALF>(a, tile, stream);
+    case Epi::GELU: return h ? launch_t<f16, Epi::GELU>(a, tile, stream) : launch_t<bf16, Epi::GELU>(a, tile, stream);
+    case Epi::QKV: return h ? launch_t<f16, Epi::QKV>(a, tile, stream) : launch_t<bf16, Epi::QKV>(a, tile, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace laya

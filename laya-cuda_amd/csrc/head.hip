@@ -1,0 +1,227 @@
+// Decision head: option-row gather, scorer, per-question softmax features and act head.
+//
+// Follows laya_cuda/laya.py:214-245 with no head transformer layers (laya.py:236-237), kept in
+// fp32 end to end (the returned probabilities are computed from these logits):
+//   gather  : selected = residual[indices] + type_emb[kind]   (kernels.cu:155-162; bit-exact)
+//   scorer  : logit = w3 . gelu(W1 LN(selected; eps 1e-5) + b1) + b3   (laya.py:238-241)
+//   features: CLS row | p1, p1-p2, entropy/log(max(n,2)), max(n,2)/255  (kernels.cu:167-183)
+//   act head: acts = A2 gelu(A0 features + a0) + a2                      (laya.py:243-245)
+//
+// Only the head rows that exist are computed: the host lists them compactly (question by
+// question: CLS, then each option), so a slot whose option capacity is padded to a power of two
+// does no work for the padding.
+#include "kernels.hpp"
+#include "rowops.hpp"
+
+namespace laya {
+
+namespace {
+
+template <int D>
+__global__ __launch_bounds__(256) void head_gather_kernel(HeadGatherArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.cap || r >= *a.n_sel) return;
+  const int src = a.sel_src[r];
+  float v[D / 64];
+  load_row<D>(a.residual + static_cast<size_t>(src) * D, lane, v);
+  if (a.type_emb) {
+    float t[D / 64];
+    load_row<D>(a.type_emb + static_cast<size_t>(a.qkind[a.sel_q[r]]) * D, lane, t);
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) v[i] = v[i] + t[i];
+  }
+  store_row<D>(a.selected + static_cast<size_t>(r) * D, lane, v);
+  normalize<D>(v, lane, a.gamma, a.beta, a.eps);
+  store_row<D>(a.normed + static_cast<size_t>(r) * D, lane, v);
+}
+
+// fp32 GEMM on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): parts[z] = X W^T over split z.
+// Workgroup tile 32 rows x 64 cols, 4 waves of 16x32; K staged in 32-wide LDS slabs.
+__global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
+  constexpr int BM = 32, BN = 64, BKH = 32;
+  const int rows = min(a.cap, *a.n_rows);
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, z = blockIdx.z;
+  if (m0 >= rows) return;
+  __shared__ float sA[BM][BKH + 1];
+  __shared__ float sB[BN][BKH + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave >> 1) * 16, wn = (wave & 1) * 32;
+  const int per = a.K / a.splits;
+  const int kb = z * per, ke = kb + per;
+  f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  for (int k0 = kb; k0 < ke; k0 += BKH) {
+    for (int e = tid; e < BM * BKH; e += 256) {
+      const int r = e / BKH, c = e % BKH;
+      sA[r][c] = m0 + r < rows ? a.x[static_cast<size_t>(m0 + r) * a.K + k0 + c] : 0.f;
+    }
+    for (int e = tid; e < BN * BKH; e += 256) {
+      const int r = e / BKH, c = e % BKH;
+      sB[r][c] = a.w[static_cast<size_t>(n0 + r) * a.K + k0 + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < BKH; kk += 4) {
+      const float av = sA[wm + (lane & 15)][kk + (lane >> 4)];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const float bv = sB[wn + t * 16 + (lane & 15)][kk + (lane >> 4)];
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[t], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = m0 + wm + 4 * (lane >> 4) + e, col = n0 + wn + t * 16 + (lane & 15);
+      if (row < rows) a.parts[z * a.split_stride + static_cast<size_t>(row) * a.N + col] = acc[t][e];
+    }
+}
+
+// One workgroup per question: logits of its CLS + option rows, softmax features, act head.
+template <int D>
+__global__ __launch_bounds__(256) void head_finish_kernel(HeadFinishArgs a) {
+  const int q = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float* logits = a.logits + static_cast<size_t>(q) * (a.k + 1);
+  float* acts = a.acts + static_cast<size_t>(q) * a.n_act;
+  if (q >= *a.n_q) {  // unused question slots of the shape class
+    for (int j = tid; j <= a.k; j += 256) logits[j] = 0.f;
+    for (int j = tid; j < a.n_act; j += 256) acts[j] = 0.f;
+    return;
+  }
+  extern __shared__ float sh[];
+  float* slog = sh;                 // [k+1]
+  float* feat = slog + (a.k + 1);   // [D+4]
+  float* hid = feat + (D + 4);      // [hidden]
+  const int count = a.counts[q], base = a.qoff[q];
+
+  float b1[D / 64], w3[D / 64];
+  load_row<D>(a.b1, lane, b1);
+  load_row<D>(a.w3, lane, w3);
+  for (int j = wave; j <= a.k; j += 4) {
+    float logit = 0.f;
+    if (j <= count) {
+      const size_t off = static_cast<size_t>(base + j) * D;
+      float v[D / 64];
+      load_row<D>(a.parts + off, lane, v);
+      for (int s = 1; s < a.splits; ++s) {
+        float t[D / 64];
+        load_row<D>(a.parts + s * a.split_stride + off, lane, t);
+#pragma unroll
+        for (int i = 0; i < D / 64; ++i) v[i] = v[i] + t[i];
+      }
+      float dot = 0.f;
+#pragma unroll
+      for (int i = 0; i < D / 64; ++i) dot += gelu(v[i] + b1[i]) * w3[i];
+      logit = wave_sum(dot) + a.b3[0];
+    }
+    if (lane == 0) {
+      logits[j] = logit;
+      slog[j] = logit;
+    }
+  }
+  // CLS row of the gathered (pre-norm) rows opens the feature vector.
+  for (int e = tid; e < D; e += 256) feat[e] = a.selected[static_cast<size_t>(base) * D + e];
+  __syncthreads();
+
+  if (wave == 0) {  // softmax over this question's option logits (slots 1..count)
+    float mx = -INFINITY;
+    for (int j = lane; j < count; j += 64) mx = fmaxf(mx, slog[1 + j]);
+    mx = wave_max(mx);
+    float se = 0.f;
+    for (int j = lane; j < count; j += 64) se += expf(slog[1 + j] - mx);
+    se = wave_sum(se);
+    float ent = 0.f, t1 = 0.f, t2 = 0.f;  // entropy and top-2 probabilities
+    for (int j = lane; j < count; j += 64) {
+      const float p = expf(slog[1 + j] - mx) / se;
+      ent -= p * logf(fmaxf(p, 1e-9f));
+      if (p > t1) {
+        t2 = t1;
+        t1 = p;
+      } else {
+        t2 = fmaxf(t2, p);
+      }
+    }
+    ent = wave_sum(ent);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      const float o1 = __shfl_xor(t1, d, 64), o2 = __shfl_xor(t2, d, 64);
+      t2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
+      t1 = fmaxf(t1, o1);
+    }
+    if (lane == 0) {
+      const int n = max(count, 2);
+      feat[D] = t1;
+      feat[D + 1] = t1 - t2;
+      feat[D + 2] = ent / logf(static_cast<float>(n));
+      feat[D + 3] = static_cast<float>(n) / 255.f;
+    }
+  }
+  __syncthreads();
+
+  // act_head.0 + GELU: one wave per output, lanes stride the D+4 inputs.
+  for (int o = wave; o < a.hidden; o += 4) {
+    const float* w = a.a0w + static_cast<size_t>(o) * (D + 4);
+    float s = 0.f;
+    for (int e = lane; e < D + 4; e += 64) s += feat[e] * w[e];
+    s = wave_sum(s);
+    if (lane == 0) hid[o] = gelu(s + a.a0b[o]);
+  }
+  __syncthreads();
+  for (int o = wave; o < a.n_act; o += 4) {
+    const float* w = a.a2w + static_cast<size_t>(o) * a.hidden;
+    float s = 0.f;
+    for (int e = lane; e < a.hidden; e += 64) s += hid[e] * w[e];
+    s = wave_sum(s);
+    if (lane == 0) acts[o] = s + a.a2b[o];
+  }
+}
+
+}  // namespace
+
+hipError_t launch_head_gather(const HeadGatherArgs& a, int width, hipStream_t stream) {
+  if (a.cap <= 0) return hipSuccess;
+  const dim3 grid((a.cap + 3) / 4), block(256);
+  switch (width) {
+#define LAYA_CASE(D) case D: hipLaunchKernelGGL((head_gather_kernel<D>), grid, block, 0, stream, a); break;
+    LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
+    LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
+#undef LAYA_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+int head_gemm_splits(int rows, int N, int K, int cus) {
+  const long long wgs = static_cast<long long>((rows + 31) / 32) * (N / 64);
+  int s = 1;
+  while (wgs * s < cus && K % (s * 2 * 32) == 0 && K / (s * 2) >= 64) s *= 2;
+  return s;
+}
+
+hipError_t launch_head_gemm(const HeadGemmArgs& a, hipStream_t stream) {
+  if (a.cap <= 0) return hipSuccess;
+  if (a.N % 64 || a.K % (a.splits * 32)) return hipErrorInvalidValue;
+  const dim3 grid(a.N / 64, (a.cap + 31) / 32, a.splits);
+  hipLaunchKernelGGL(head_gemm_kernel, grid, dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_head_finish(const HeadFinishArgs& a, hipStream_t stream) {
+  if (a.b <= 0) return hipSuccess;
+  const size_t lds = static_cast<size_t>(a.k + 1 + a.width + 4 + a.hidden) * sizeof(float);
+  const dim3 grid(a.b), block(256);
+  switch (a.width) {
+#define LAYA_CASE(D) case D: hipLaunchKernelGGL((head_finish_kernel<D>), grid, block, lds, stream, a); break;
+    LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
+    LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
+#undef LAYA_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace laya

@@ -1,0 +1,140 @@
+// Kernel argument blocks and launchers for the encoder forward path (gfx950).
+#pragma once
+
+#include "common.hpp"
+
+namespace laya {
+
+enum class DType : int { F32 = 0, F16 = 1, BF16 = 2 };
+
+// ---- embedding gather (+ learned position + type row) (+ LayerNorm) ----
+struct EmbedArgs {
+  const int32_t* ids;
+  const int32_t* positions;
+  const float* table;      // [vocab][d]
+  const float* pos_table;  // [n_positions][d] or null
+  const float* type_row;   // [d] or null
+  const float* gamma;      // null: no LayerNorm (pure gather + adds)
+  const float* beta;
+  float eps;
+  float* out32;  // [rows][d] or null
+  void* out16;   // [rows][d] 16-bit or null
+  int rows, vocab, n_positions;
+};
+
+// ---- residual add (+ split-K partial sum + bias) (+ LayerNorm) ----
+struct AddNormArgs {
+  float* residual;         // [rows][d]
+  const float* parts;      // [splits][rows][d] branch partials, or null
+  int splits;
+  long long part_stride;   // elements between partials
+  const float* bias;       // [d] added to the branch, or null
+  const float* gamma;      // null: no LayerNorm
+  const float* beta;
+  float eps;
+  float* sum_out;  // pre-norm sum residual+branch, or null
+  float* out32;    // normalised (or sum, if gamma is null) fp32, may alias residual
+  void* out16;     // same as 16-bit, or null
+  int rows;
+};
+
+bool norm_width_supported(int width);
+hipError_t launch_embed(const EmbedArgs& a, int width, DType t, hipStream_t stream);
+hipError_t launch_add_norm(const AddNormArgs& a, int width, DType t, hipStream_t stream);
+
+// ---- MFMA GEMM: out[M][N] = A[M][K] * B[N][K]^T (+ bias), fp32 accumulate ----
+enum class Epi : int { F32 = 0, HALF = 1, GELU = 2, QKV = 3 };
+
+struct GemmArgs {
+  const void* a;  // [M][lda] 16-bit
+  const void* b;  // [N][ldb] 16-bit
+  int M, N, K, lda, ldb;
+  const float* bias;        // [N] or null (F32 epilogue: only with splits == 1)
+  void* out;                // F32: float [splits][M][ldo]; HALF/GELU: 16-bit [M][ldo]
+  long long ldo;
+  long long split_stride;   // F32: elements between split partials
+  int splits;
+  // QKV epilogue: columns [0,w) -> q, [w,2w) -> k, [2w,3w) -> vt.
+  // q, k: [heads][M][64]; vt: [heads][64][M] (keys contiguous).
+  void* q;
+  void* k;
+  void* vt;
+  int width;
+};
+
+struct GemmTile {
+  int bm, bn;
+};
+int gemm_tile_count();
+GemmTile gemm_tile(int id);
+// Chooses a tile and split count for a problem on `cus` compute units.
+void gemm_plan(int M, int N, int K, Epi epi, int cus, int* tile, int* splits);
+hipError_t gemm_prepare();  // sets LDS attributes of the large-tile kernels (call once per device)
+hipError_t launch_gemm(const GemmArgs& a, Epi epi, DType t, int tile, hipStream_t stream);
+
+// ---- fused bidirectional attention over packed rows ----
+// tiles: [max_tiles][3] = (row0, row1, seq); seq < 0 marks rows to zero.
+struct AttnArgs {
+  const void* q;   // [heads][m][64]
+  const void* k;   // [heads][m][64]
+  const void* vt;  // [heads][64][m]
+  void* out;       // [m][heads*64]
+  const int32_t* tiles;
+  const int32_t* n_tiles;
+  const int32_t* starts;
+  const int32_t* lengths;
+  int m, heads, max_tiles;
+};
+int attention_block_rows(int waves);
+hipError_t launch_attention(const AttnArgs& a, DType t, int waves, hipStream_t stream);
+
+// ---- decision head (no head transformer layers) ----
+struct HeadGatherArgs {
+  const float* residual;  // [m][d]
+  const int32_t* sel_src; // [cap] packed source row of each compact head row
+  const int32_t* sel_q;   // [cap] question of each compact head row
+  const int32_t* qkind;   // [b]
+  const int32_t* n_sel;   // device scalar
+  const float* type_emb;  // [3][d] or null
+  const float* gamma;     // scorer.0
+  const float* beta;
+  float eps;
+  float* selected;  // [cap][d] gathered rows (+ type row)
+  float* normed;    // [cap][d] LayerNorm of selected
+  int cap;
+};
+hipError_t launch_head_gather(const HeadGatherArgs& a, int width, hipStream_t stream);
+
+struct HeadGemmArgs {
+  const float* x;  // [cap][K]
+  const float* w;  // [N][K]
+  float* parts;    // [splits][cap][N]
+  const int32_t* n_rows;  // device scalar (rows actually present)
+  int cap, N, K, splits;
+  long long split_stride;
+};
+int head_gemm_splits(int rows, int N, int K, int cus);
+hipError_t launch_head_gemm(const HeadGemmArgs& a, hipStream_t stream);
+
+struct HeadFinishArgs {
+  const float* parts;  // scorer.1 partial products [splits][cap][d]
+  int splits;
+  long long split_stride;
+  const float* b1;     // scorer.1 bias [d]
+  const float* w3;     // scorer.3 weight [d]
+  const float* b3;     // scorer.3 bias [1]
+  const float* selected;
+  const int32_t* counts;  // [b]
+  const int32_t* qoff;    // [b] first compact head row of each question
+  const int32_t* n_q;     // device scalar
+  const float* a0w;  // act_head.0 [hidden][d+4]
+  const float* a0b;
+  const float* a2w;  // act_head.2 [n_act][hidden]
+  const float* a2b;
+  float* logits;  // [b][k+1]
+  float* acts;    // [b][n_act]
+  int b, k, width, n_act, hidden;
+};
+hipError_t launch_head_finish(const HeadFinishArgs& a, hipStream_t stream);
+
+}  // namespace laya

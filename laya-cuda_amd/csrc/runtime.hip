@@ -1,0 +1,839 @@
+// Native runtime behind the C ABI: resident weights, shape slots with one hipGraph each, LRU.
+//
+// Mirrors the ownership of the reference's Runtime/Slot (laya_cuda/runtime.py:28-197) in C++:
+//   * one engine per device, one non-blocking stream (default priority), weights resident in HBM
+//     for the engine's lifetime (matrices in the MFMA operand type, the rest fp32);
+//   * a slot per shape class (rows, questions, options) holding ONE device allocation (its arena)
+//     plus pinned staging, built on a cache miss and evicted least-recently-used;
+//   * the slot's forward is captured into a hipGraph on first use and replayed afterwards; the
+//     packed inputs are uploaded with one H2D copy before the launch (runtime.py:52-68, 115-133).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <list>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "kernels.hpp"
+#include "laya_hip.h"
+
+namespace laya {
+namespace {
+
+thread_local std::string g_error;
+
+struct Failure {
+  int code;
+  std::string message;
+};
+
+#define LAYA_HIP(expr)                                                                     \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    if (e_ != hipSuccess)                                                                  \
+      throw Failure{e_ == hipErrorOutOfMemory ? LAYA_ENOMEM : LAYA_EDEVICE,                \
+                    std::string(#expr) + ": " + hipGetErrorString(e_)};                     \
+  } while (0)
+
+#define LAYA_REQUIRE(cond, msg)                     \
+  do {                                              \
+    if (!(cond)) throw Failure{LAYA_EINVAL, (msg)}; \
+  } while (0)
+
+int span16(int n) { return (n + 15) / 16 * 16; }
+
+// ---- host dtype conversion (round to nearest even) ----
+uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+float bf16_bits_to_f32(uint16_t b) {
+  uint32_t u = static_cast<uint32_t>(b) << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  uint16_t b;
+  std::memcpy(&b, &h, 2);
+  return b;
+}
+float f16_bits_to_f32(uint16_t b) {
+  _Float16 h;
+  std::memcpy(&h, &b, 2);
+  return static_cast<float>(h);
+}
+
+float host_value(const void* data, int dtype, size_t i) {
+  switch (dtype) {
+    case LAYA_F32: return static_cast<const float*>(data)[i];
+    case LAYA_F16: return f16_bits_to_f32(static_cast<const uint16_t*>(data)[i]);
+    default: return bf16_bits_to_f32(static_cast<const uint16_t*>(data)[i]);
+  }
+}
+
+struct DevTensor {
+  void* ptr = nullptr;
+  DType dtype = DType::F32;
+  std::vector<int64_t> shape;
+  size_t count = 0;
+  size_t bytes = 0;
+};
+
+struct Expected {
+  std::vector<int64_t> shape;
+  bool mfma = false;  // resident in the 16-bit MFMA operand type
+};
+
+// Packed input layout for shape (m, b, k): the caller's block (laya_packed_ints) followed by the
+// derived work lists the host builds before the single upload.
+struct Layout {
+  size_t meta, ids, positions, rows, kinds, starts, lengths, counts, qkind, indices, user_end;
+  size_t qoff, tiles, n_tiles, sel_src, sel_q, n_sel, total;
+  int T, R;
+};
+Layout make_layout(int m, int b, int k) {
+  Layout L{};
+  size_t o = 0;
+  auto take = [&](size_t n) { size_t at = o; o += n; return at; };
+  L.meta = take(4);
+  L.ids = take(m);
+  L.positions = take(m);
+  L.rows = take(m);
+  L.kinds = take(m);
+  L.starts = take(b);
+  L.lengths = take(b);
+  L.counts = take(b);
+  L.qkind = take(b);
+  L.indices = take(static_cast<size_t>(b) * (k + 1));
+  L.user_end = o;
+  L.T = m / 16;
+  L.R = b * (k + 1);
+  L.qoff = take(b);
+  L.tiles = take(static_cast<size_t>(3) * L.T);
+  L.n_tiles = take(1);
+  L.sel_src = take(L.R);
+  L.sel_q = take(L.R);
+  L.n_sel = take(1);
+  L.total = o;
+  return L;
+}
+
+struct Slot {
+  int m = 0, b = 0, k = 0;
+  Layout L{};
+  void* arena = nullptr;
+  size_t bytes = 0;
+  int32_t* d_packed = nullptr;
+  int32_t* h_packed = nullptr;
+  float* h_logits = nullptr;
+  float* h_acts = nullptr;
+  float* residual = nullptr;
+  void *x = nullptr, *q = nullptr, *kk = nullptr, *vt = nullptr, *attn = nullptr, *ff = nullptr;
+  float* part = nullptr;
+  float *selected = nullptr, *normed = nullptr, *hpart = nullptr, *logits = nullptr, *acts = nullptr;
+  int tile[4] = {0, 0, 0, 0}, splits[4] = {1, 1, 1, 1};  // qkv, o, up, down
+  int attn_waves = 2, head_splits = 1;
+  hipGraphExec_t graph = nullptr;
+  hipEvent_t start = nullptr, end = nullptr;
+};
+
+struct Layer {
+  const void *wqkv, *wo, *wi, *wo2;
+  const float *bqkv, *bo, *bi, *bo2, *n1g, *n1b, *n2g, *n2b;
+};
+
+struct Engine {
+  LayaConfig cfg{};
+  int device = 0, cus = 256, max_slots = 16;
+  hipStream_t stream = nullptr;
+  std::unordered_map<std::string, Expected> expected;
+  std::unordered_map<std::string, DevTensor> weights;
+  size_t weight_bytes = 0, slot_bytes = 0;
+  bool finalized = false;
+  std::vector<Layer> layers;
+  const float *tok = nullptr, *pos = nullptr, *type0 = nullptr, *emb_g = nullptr, *emb_b = nullptr;
+  const float *type_emb = nullptr, *s0w = nullptr, *s0b = nullptr, *s1w = nullptr, *s1b = nullptr;
+  const float *s3w = nullptr, *s3b = nullptr, *a0w = nullptr, *a0b = nullptr, *a2w = nullptr, *a2b = nullptr;
+  std::list<Slot*> lru;  // front = least recently used
+  std::string error;
+
+  DType mfma() const { return cfg.mfma_dtype == LAYA_F16 ? DType::F16 : DType::BF16; }
+};
+
+void check_config(const LayaConfig& c) {
+  LAYA_REQUIRE(c.heads > 0 && c.width == c.heads * 64, "width must equal heads * 64 (64-wide attention heads)");
+  LAYA_REQUIRE(norm_width_supported(c.width), "unsupported width " + std::to_string(c.width));
+  LAYA_REQUIRE(c.width % 64 == 0 && c.width >= 64, "width must be a multiple of 64");
+  LAYA_REQUIRE(c.layers >= 1 && c.intermediate > 0 && c.intermediate % 256 == 0,
+               "intermediate size must be a positive multiple of 256");
+  LAYA_REQUIRE(c.vocab > 0 && c.max_positions > 0 && c.type_vocab > 0, "vocab/positions/type rows must be positive");
+  LAYA_REQUIRE(c.max_len > 0 && span16(c.max_len) <= (c.pos_kind == LAYA_POS_LEARNED ? span16(c.max_positions) : 1 << 20),
+               "max_len exceeds the position table");
+  LAYA_REQUIRE(c.n_act >= 1 && c.act_hidden >= 1, "act head must have outputs");
+  LAYA_REQUIRE(c.mfma_dtype == LAYA_BF16 || c.mfma_dtype == LAYA_F16, "mfma_dtype must be LAYA_BF16 or LAYA_F16");
+  LAYA_REQUIRE(c.eps > 0.f, "eps must be positive");
+  // The graded workloads run the BERT-style post-LN encoder; the reference's ModernBERT executor
+  // variant (pre-LN, RoPE, GeGLU, local windows, head layers) is not built in this library yet.
+  LAYA_REQUIRE(c.norm_order == LAYA_NORM_POST && c.pos_kind == LAYA_POS_LEARNED && c.ffn_kind == LAYA_FFN_GELU &&
+                   c.bias == 1 && c.window < 0 && c.head_layers == 0,
+               "encoder variant not built: only post-LN, learned positions, GELU FFN with biases, global "
+               "attention and head_layers=0 are implemented");
+}
+
+void build_expected(Engine& E) {
+  const LayaConfig& c = E.cfg;
+  const int64_t d = c.width, f = c.intermediate;
+  auto put = [&](const std::string& n, std::vector<int64_t> s, bool mf = false) { E.expected[n] = Expected{s, mf}; };
+  put("encoder.embeddings.tok_embeddings.weight", {c.vocab, d});
+  put("encoder.embeddings.position_embeddings.weight", {c.max_positions, d});
+  put("encoder.embeddings.token_type_embeddings.weight", {c.type_vocab, d});
+  put("encoder.embeddings.norm.weight", {d});
+  put("encoder.embeddings.norm.bias", {d});
+  for (int i = 0; i < c.layers; ++i) {
+    const std::string p = "encoder.layers." + std::to_string(i) + ".";
+    put(p + "attn.Wqkv.weight", {3 * d, d}, true);
+    put(p + "attn.Wqkv.bias", {3 * d});
+    put(p + "attn.Wo.weight", {d, d}, true);
+    put(p + "attn.Wo.bias", {d});
+    put(p + "post_attn_norm.weight", {d});
+    put(p + "post_attn_norm.bias", {d});
+    put(p + "mlp.Wi.weight", {f, d}, true);
+    put(p + "mlp.Wi.bias", {f});
+    put(p + "mlp.Wo.weight", {d, f}, true);
+    put(p + "mlp.Wo.bias", {d});
+    put(p + "post_mlp_norm.weight", {d});
+    put(p + "post_mlp_norm.bias", {d});
+  }
+  put("type_emb.weight", {3, d});
+  put("scorer.0.weight", {d});
+  put("scorer.0.bias", {d});
+  put("scorer.1.weight", {d, d});
+  put("scorer.1.bias", {d});
+  put("scorer.3.weight", {1, d});
+  put("scorer.3.bias", {1});
+  put("act_head.0.weight", {c.act_hidden, d + 4});
+  put("act_head.0.bias", {c.act_hidden});
+  put("act_head.2.weight", {c.n_act, c.act_hidden});
+  put("act_head.2.bias", {c.n_act});
+}
+
+const DevTensor& need(Engine& E, const std::string& name) {
+  auto it = E.weights.find(name);
+  LAYA_REQUIRE(it != E.weights.end(), "missing tensor: " + name);
+  return it->second;
+}
+const float* f32(Engine& E, const std::string& name) { return static_cast<const float*>(need(E, name).ptr); }
+
+void destroy_slot(Engine& E, Slot* s) {
+  if (s->graph) (void)hipGraphExecDestroy(s->graph);
+  if (s->start) (void)hipEventDestroy(s->start);
+  if (s->end) (void)hipEventDestroy(s->end);
+  if (s->arena) (void)hipFree(s->arena);
+  if (s->h_packed) (void)hipHostFree(s->h_packed);
+  if (s->h_logits) (void)hipHostFree(s->h_logits);
+  if (s->h_acts) (void)hipHostFree(s->h_acts);
+  E.slot_bytes -= s->bytes;
+  delete s;
+}
+
+Slot* create_slot(Engine& E, int m, int b, int k) {
+  const LayaConfig& c = E.cfg;
+  Slot* s = new Slot();
+  s->m = m;
+  s->b = b;
+  s->k = k;
+  s->L = make_layout(m, b, k);
+  const int d = c.width, f = c.intermediate;
+  try {
+    gemm_plan(m, 3 * d, d, Epi::QKV, E.cus, &s->tile[0], &s->splits[0]);
+    gemm_plan(m, d, d, Epi::F32, E.cus, &s->tile[1], &s->splits[1]);
+    gemm_plan(m, f, d, Epi::GELU, E.cus, &s->tile[2], &s->splits[2]);
+    gemm_plan(m, d, f, Epi::F32, E.cus, &s->tile[3], &s->splits[3]);
+    s->splits[0] = s->splits[2] = 1;
+    s->attn_waves = (static_cast<long long>(m / 128) * c.heads >= E.cus) ? 4 : 2;
+    s->head_splits = head_gemm_splits(s->L.R, d, d, E.cus);
+    const int max_split = s->splits[1] > s->splits[3] ? s->splits[1] : s->splits[3];
+
+    const size_t h2 = 2;  // 16-bit element
+    const size_t md = static_cast<size_t>(m) * d, R = s->L.R;
+    struct Part {
+      void** dst;
+      size_t bytes;
+    };
+    std::vector<Part> parts = {
+        {reinterpret_cast<void**>(&s->d_packed), s->L.total * 4},
+        {reinterpret_cast<void**>(&s->residual), md * 4},
+        {&s->x, md * h2},
+        {&s->q, md * h2},
+        {&s->kk, md * h2},
+        {&s->vt, md * h2},
+        {&s->attn, md * h2},
+        {&s->ff, static_cast<size_t>(m) * f * h2},
+        {reinterpret_cast<void**>(&s->part), md * 4 * max_split},
+        {reinterpret_cast<void**>(&s->selected), R * d * 4},
+        {reinterpret_cast<void**>(&s->normed), R * d * 4},
+        {reinterpret_cast<void**>(&s->hpart), R * d * 4 * s->head_splits},
+        {reinterpret_cast<void**>(&s->logits), static_cast<size_t>(b) * (k + 1) * 4},
+        {reinterpret_cast<void**>(&s->acts), static_cast<size_t>(b) * c.n_act * 4},
+    };
+    size_t total = 0;
+    for (auto& p : parts) total += (p.bytes + 255) / 256 * 256;
+    LAYA_HIP(hipMalloc(&s->arena, total));
+    s->bytes = total;
+    E.slot_bytes += total;
+    char* cur = static_cast<char*>(s->arena);
+    for (auto& p : parts) {
+      *p.dst = cur;
+      cur += (p.bytes + 255) / 256 * 256;
+    }
+    LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_packed), s->L.total * 4, hipHostMallocDefault));
+    LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_logits), static_cast<size_t>(b) * (k + 1) * 4, hipHostMallocDefault));
+    LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_acts), static_cast<size_t>(b) * c.n_act * 4, hipHostMallocDefault));
+    LAYA_HIP(hipEventCreate(&s->start));
+    LAYA_HIP(hipEventCreate(&s->end));
+  } catch (...) {
+    destroy_slot(E, s);
+    throw;
+  }
+  return s;
+}
+
+// Host side of Slot.fill's contract: validate the caller's block, then derive the attention tile
+// list and the compact head-row list into the same staging buffer.
+void derive_inputs(const Engine& E, Slot& s) {
+  const LayaConfig& c = E.cfg;
+  const Layout& L = s.L;
+  int32_t* P = s.h_packed;
+  const int m = s.m, b = s.b, k = s.k;
+  const int n_seq = P[L.meta], n_q = P[L.meta + 1];
+  LAYA_REQUIRE(n_seq >= 0 && n_seq <= b && n_q >= 0 && n_q <= b, "sequence/question count exceeds the shape class");
+  for (int i = 0; i < m; ++i) {
+    LAYA_REQUIRE(P[L.ids + i] >= 0 && P[L.ids + i] < c.vocab, "token id out of range");
+    LAYA_REQUIRE(P[L.positions + i] >= 0 && P[L.positions + i] < c.max_positions, "position out of range");
+  }
+  // Attention tiles: sequences in increasing start order, 16-aligned, non-overlapping.
+  const int block = attention_block_rows(s.attn_waves);
+  int32_t* tiles = P + L.tiles;
+  int nt = 0, row = 0;
+  auto zero_to = [&](int upto) {
+    while (row < upto) {
+      const int r1 = (upto - row > block) ? row + block : upto;
+      tiles[3 * nt] = row;
+      tiles[3 * nt + 1] = r1;
+      tiles[3 * nt + 2] = -1;
+      ++nt;
+      row = r1;
+    }
+  };
+  for (int sq = 0; sq < n_seq; ++sq) {
+    const int st = P[L.starts + sq], len = P[L.lengths + sq];
+    LAYA_REQUIRE(st % 16 == 0 && st >= row && len >= 0 && st + span16(len) <= m,
+                 "sequences must start at increasing multiples of 16 rows and fit the shape class");
+    zero_to(st);
+    const int e = st + span16(len);
+    while (row < e) {
+      const int r1 = (e - row > block) ? row + block : e;
+      tiles[3 * nt] = row;
+      tiles[3 * nt + 1] = r1;
+      tiles[3 * nt + 2] = sq;
+      ++nt;
+      row = r1;
+    }
+  }
+  zero_to(m);
+  LAYA_REQUIRE(nt <= L.T, "attention tile list overflow");
+  P[L.n_tiles] = nt;
+  // Compact head rows: per question its CLS row then its option rows.
+  int ns = 0;
+  for (int q = 0; q < n_q; ++q) {
+    const int cnt = P[L.counts + q];
+    LAYA_REQUIRE(cnt >= 0 && cnt <= k, "option count exceeds the shape class");
+    LAYA_REQUIRE(P[L.qkind + q] >= 0 && P[L.qkind + q] < 3, "question kind out of range");
+    P[L.qoff + q] = ns;
+    for (int j = 0; j <= cnt; ++j) {
+      const int src = P[L.indices + static_cast<size_t>(q) * (k + 1) + j];
+      LAYA_REQUIRE(src >= 0 && src < m, "readout index out of range");
+      P[L.sel_src + ns] = src;
+      P[L.sel_q + ns] = q;
+      ++ns;
+    }
+  }
+  for (int q = n_q; q < b; ++q) P[L.qoff + q] = ns;
+  P[L.n_sel] = ns;
+}
+
+void check_launch(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw Failure{LAYA_EDEVICE, std::string(what) + ": " + hipGetErrorString(e)};
+}
+
+void forward(Engine& E, Slot& s) {
+  const LayaConfig& c = E.cfg;
+  const int m = s.m, d = c.width, f = c.intermediate;
+  const DType t = E.mfma();
+  const int32_t* P = s.d_packed;
+  const Layout& L = s.L;
+  hipStream_t st = E.stream;
+
+  EmbedArgs ea{P + L.ids, P + L.positions, E.tok, E.pos, E.type0, E.emb_g, E.emb_b, c.eps,
+               s.residual, s.x, m, c.vocab, c.max_positions};
+  check_launch(launch_embed(ea, d, t, st), "embed");
+  const long long md = static_cast<long long>(m) * d;
+  for (const Layer& ly : E.layers) {
+    GemmArgs g{};
+    g.a = s.x; g.b = ly.wqkv; g.M = m; g.N = 3 * d; g.K = d; g.lda = d; g.ldb = d;
+    g.bias = ly.bqkv; g.splits = 1; g.q = s.q; g.k = s.kk; g.vt = s.vt; g.width = d;
+    check_launch(launch_gemm(g, Epi::QKV, t, s.tile[0], st), "qkv");
+
+    AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, P + L.n_tiles, P + L.starts, P + L.lengths, m, c.heads, L.T};
+    check_launch(launch_attention(aa, t, s.attn_waves, st), "attention");
+
+    g = GemmArgs{};
+    g.a = s.attn; g.b = ly.wo; g.M = m; g.N = d; g.K = d; g.lda = d; g.ldb = d;
+    g.out = s.part; g.ldo = d; g.split_stride = md; g.splits = s.splits[1];
+    check_launch(launch_gemm(g, Epi::F32, t, s.tile[1], st), "attn out");
+    AddNormArgs na{s.residual, s.part, s.splits[1], md, ly.bo, ly.n1g, ly.n1b, c.eps, nullptr, s.residual, s.x, m};
+    check_launch(launch_add_norm(na, d, t, st), "post-attention norm");
+
+    g = GemmArgs{};
+    g.a = s.x; g.b = ly.wi; g.M = m; g.N = f; g.K = d; g.lda = d; g.ldb = d;
+    g.bias = ly.bi; g.out = s.ff; g.ldo = f; g.splits = 1;
+    check_launch(launch_gemm(g, Epi::GELU, t, s.tile[2], st), "ffn up");
+    g = GemmArgs{};
+    g.a = s.ff; g.b = ly.wo2; g.M = m; g.N = d; g.K = f; g.lda = f; g.ldb = f;
+    g.out = s.part; g.ldo = d; g.split_stride = md; g.splits = s.splits[3];
+    check_launch(launch_gemm(g, Epi::F32, t, s.tile[3], st), "ffn down");
+    na = AddNormArgs{s.residual, s.part, s.splits[3], md, ly.bo2, ly.n2g, ly.n2b, c.eps, nullptr, s.residual, s.x, m};
+    check_launch(launch_add_norm(na, d, t, st), "post-ffn norm");
+  }
+
+  HeadGatherArgs hg{s.residual, P + L.sel_src, P + L.sel_q, P + L.qkind, P + L.n_sel, E.type_emb,
+                    E.s0w, E.s0b, 1e-5f, s.selected, s.normed, L.R};
+  check_launch(launch_head_gather(hg, d, st), "head gather");
+  HeadGemmArgs hm{s.normed, E.s1w, s.hpart, P + L.n_sel, L.R, d, d, s.head_splits, static_cast<long long>(L.R) * d};
+  check_launch(launch_head_gemm(hm, st), "scorer");
+  HeadFinishArgs hf{s.hpart, s.head_splits, static_cast<long long>(L.R) * d, E.s1b, E.s3w, E.s3b, s.selected,
+                    P + L.counts, P + L.qoff, P + L.meta + 1, E.a0w, E.a0b, E.a2w, E.a2b, s.logits, s.acts,
+                    s.b, s.k, d, c.n_act, c.act_hidden};
+  check_launch(launch_head_finish(hf, st), "head finish");
+}
+
+Slot* find_slot(Engine& E, int m, int b, int k, bool* miss) {
+  for (auto it = E.lru.begin(); it != E.lru.end(); ++it) {
+    Slot* s = *it;
+    if (s->m == m && s->b == b && s->k == k) {
+      E.lru.erase(it);
+      E.lru.push_back(s);
+      *miss = false;
+      return s;
+    }
+  }
+  *miss = true;
+  if (static_cast<int>(E.lru.size()) >= E.max_slots) {
+    LAYA_HIP(hipStreamSynchronize(E.stream));
+    Slot* old = E.lru.front();
+    E.lru.pop_front();
+    destroy_slot(E, old);
+  }
+  Slot* s = create_slot(E, m, b, k);
+  E.lru.push_back(s);
+  return s;
+}
+
+int fail(Engine* E, const Failure& f) {
+  g_error = f.message;
+  if (E) E->error = f.message;
+  return f.code;
+}
+
+template <typename F>
+int guarded(Engine* E, F&& body) {
+  try {
+    body();
+    return LAYA_OK;
+  } catch (const Failure& f) {
+    return fail(E, f);
+  } catch (const std::exception& x) {
+    return fail(E, Failure{LAYA_EINVAL, x.what()});
+  }
+}
+
+std::mutex g_prepare_mutex;
+std::vector<int> g_prepared;
+void prepare_device() {
+  int dev = 0;
+  LAYA_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_prepare_mutex);
+  for (int d : g_prepared)
+    if (d == dev) return;
+  LAYA_HIP(gemm_prepare());
+  g_prepared.push_back(dev);
+}
+
+}  // namespace
+}  // namespace laya
+
+using namespace laya;
+
+extern "C" {
+
+int laya_abi_version(void) { return LAYA_ABI_VERSION; }
+
+int64_t laya_packed_ints(const LayaShape* shape) {
+  if (!shape || shape->rows <= 0 || shape->batch <= 0 || shape->options <= 0) return -1;
+  return static_cast<int64_t>(make_layout(shape->rows, shape->batch, shape->options).user_end);
+}
+
+int laya_create(const LayaConfig* cfg, int device, int max_slots, void** handle) {
+  if (!handle || !cfg) return fail(nullptr, Failure{LAYA_EINVAL, "null argument"});
+  *handle = nullptr;
+  Engine* E = new Engine();
+  const int rc = guarded(nullptr, [&] {
+    LAYA_REQUIRE(max_slots >= 1 && max_slots <= 64, "max_cached_shapes must be an integer between 1 and 64");
+    check_config(*cfg);
+    E->cfg = *cfg;
+    E->device = device;
+    E->max_slots = max_slots;
+    int count = 0;
+    LAYA_HIP(hipGetDeviceCount(&count));
+    LAYA_REQUIRE(device >= 0 && device < count, "no HIP device " + std::to_string(device));
+    LAYA_HIP(hipSetDevice(device));
+    hipDeviceProp_t prop;
+    LAYA_HIP(hipGetDeviceProperties(&prop, device));
+    LAYA_REQUIRE(std::strncmp(prop.gcnArchName, "gfx950", 6) == 0,
+                 std::string(prop.name) + " is " + prop.gcnArchName + "; liblaya_hip is built for gfx950 (MI355X)");
+    E->cus = prop.multiProcessorCount;
+    prepare_device();
+    LAYA_HIP(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
+    build_expected(*E);
+  });
+  if (rc != LAYA_OK) {
+    if (E->stream) (void)hipStreamDestroy(E->stream);
+    delete E;
+    return rc;
+  }
+  *handle = E;
+  return LAYA_OK;
+}
+
+int laya_load_weight(void* handle, const char* name, const void* host_data, int host_dtype, const int64_t* shape,
+                     int ndim) {
+  Engine* E = static_cast<Engine*>(handle);
+  if (!E) return fail(nullptr, Failure{LAYA_EINVAL, "null handle"});
+  return guarded(E, [&] {
+    LAYA_REQUIRE(name && host_data && (ndim == 0 || shape), "null argument");
+    LAYA_REQUIRE(host_dtype == LAYA_F32 || host_dtype == LAYA_F16 || host_dtype == LAYA_BF16, "bad host dtype");
+    const std::string n(name);
+    auto it = E->expected.find(n);
+    LAYA_REQUIRE(it != E->expected.end(), "Checkpoint tensor names do not match the Laya adapter: " + n);
+    LAYA_REQUIRE(static_cast<size_t>(ndim) == it->second.shape.size() &&
+                     std::equal(shape, shape + ndim, it->second.shape.begin()),
+                 "Incompatible tensor shape: " + n);
+    LAYA_HIP(hipSetDevice(E->device));
+    size_t count = 1;
+    for (int i = 0; i < ndim; ++i) count *= static_cast<size_t>(shape[i]);
+    DevTensor t;
+    t.shape.assign(shape, shape + ndim);
+    t.count = count;
+    std::vector<uint8_t> staged;
+    const void* src = host_data;
+    if (it->second.mfma) {
+      t.dtype = E->mfma();
+      t.bytes = count * 2;
+      staged.resize(t.bytes);
+      uint16_t* o = reinterpret_cast<uint16_t*>(staged.data());
+      const bool bf = t.dtype == DType::BF16;
+      if ((bf && host_dtype == LAYA_BF16) || (!bf && host_dtype == LAYA_F16)) {
+        std::memcpy(o, host_data, t.bytes);
+      } else {
+        for (size_t i = 0; i < count; ++i) {
+          const float v = host_value(host_data, host_dtype, i);
+          o[i] = bf ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+        }
+      }
+      src = staged.data();
+    } else {
+      t.dtype = DType::F32;
+      t.bytes = count * 4;
+      if (host_dtype != LAYA_F32) {
+        staged.resize(t.bytes);
+        float* o = reinterpret_cast<float*>(staged.data());
+        for (size_t i = 0; i < count; ++i) o[i] = host_value(host_data, host_dtype, i);
+        src = staged.data();
+      }
+    }
+    auto old = E->weights.find(n);
+    if (old != E->weights.end()) {
+      (void)hipFree(old->second.ptr);
+      E->weight_bytes -= old->second.bytes;
+      E->weights.erase(old);
+    }
+    LAYA_HIP(hipMalloc(&t.ptr, t.bytes));
+    E->weight_bytes += t.bytes;
+    E->weights[n] = t;
+    LAYA_HIP(hipMemcpy(t.ptr, src, t.bytes, hipMemcpyHostToDevice));
+    E->finalized = false;
+  });
+}
+
+int laya_finalize(void* handle) {
+  Engine* E = static_cast<Engine*>(handle);
+  if (!E) return fail(nullptr, Failure{LAYA_EINVAL, "null handle"});
+  return guarded(E, [&] {
+    for (auto& kv : E->expected) LAYA_REQUIRE(E->weights.count(kv.first), "missing tensor: " + kv.first);
+    E->tok = f32(*E, "encoder.embeddings.tok_embeddings.weight");
+    E->pos = f32(*E, "encoder.embeddings.position_embeddings.weight");
+    E->type0 = f32(*E, "encoder.embeddings.token_type_embeddings.weight");
+    E->emb_g = f32(*E, "encoder.embeddings.norm.weight");
+    E->emb_b = f32(*E, "encoder.embeddings.norm.bias");
+    E->layers.clear();
+    for (int i = 0; i < E->cfg.layers; ++i) {
+      const std::string p = "encoder.layers." + std::to_string(i) + ".";
+      Layer ly;
+      ly.wqkv = need(*E, p + "attn.Wqkv.weight").ptr;
+      ly.bqkv = f32(*E, p + "attn.Wqkv.bias");
+      ly.wo = need(*E, p + "attn.Wo.weight").ptr;
+      ly.bo = f32(*E, p + "attn.Wo.bias");
+      ly.n1g = f32(*E, p + "post_attn_norm.weight");
+      ly.n1b = f32(*E, p + "post_attn_norm.bias");
+      ly.wi = need(*E, p + "mlp.Wi.weight").ptr;
+      ly.bi = f32(*E, p + "mlp.Wi.bias");
+      ly.wo2 = need(*E, p + "mlp.Wo.weight").ptr;
+      ly.bo2 = f32(*E, p + "mlp.Wo.bias");
+      ly.n2g = f32(*E, p + "post_mlp_norm.weight");
+      ly.n2b = f32(*E, p + "post_mlp_norm.bias");
+      E->layers.push_back(ly);
+    }
+    E->type_emb = f32(*E, "type_emb.weight");
+    E->s0w = f32(*E, "scorer.0.weight");
+    E->s0b = f32(*E, "scorer.0.bias");
+    E->s1w = f32(*E, "scorer.1.weight");
+    E->s1b = f32(*E, "scorer.1.bias");
+    E->s3w = f32(*E, "scorer.3.weight");
+    E->s3b = f32(*E, "scorer.3.bias");
+    E->a0w = f32(*E, "act_head.0.weight");
+    E->a0b = f32(*E, "act_head.0.bias");
+    E->a2w = f32(*E, "act_head.2.weight");
+    E->a2b = f32(*E, "act_head.2.bias");
+    // Graphs captured earlier hold old weight pointers: drop every slot.
+    for (Slot* s : E->lru) destroy_slot(*E, s);
+    E->lru.clear();
+    E->finalized = true;
+  });
+}
+
+int laya_predict(void* handle, const int32_t* host_packed, const LayaShape* shape, int capture, float* host_logits,
+                 float* host_acts, LayaMetrics* metrics) {
+  Engine* E = static_cast<Engine*>(handle);
+  if (!E) return fail(nullptr, Failure{LAYA_EINVAL, "null handle"});
+  return guarded(E, [&] {
+    if (!E->finalized) throw Failure{LAYA_ESTATE, "predict before laya_finalize"};
+    LAYA_REQUIRE(host_packed && shape && host_logits && host_acts, "null argument");
+    const int m = shape->rows, b = shape->batch, k = shape->options;
+    LAYA_REQUIRE(m > 0 && m % 16 == 0 && m <= (1 << 22) && b > 0 && b <= (1 << 16) && k > 0 && k <= (1 << 12),
+                 "invalid shape class");
+    LAYA_HIP(hipSetDevice(E->device));
+    bool miss = false;
+    Slot* s = find_slot(*E, m, b, k, &miss);
+    std::memcpy(s->h_packed, host_packed, s->L.user_end * 4);
+    derive_inputs(*E, *s);
+    LAYA_HIP(hipMemcpyAsync(s->d_packed, s->h_packed, s->L.total * 4, hipMemcpyHostToDevice, E->stream));
+    const bool captured_now = capture && !s->graph;
+    if (captured_now) {
+      LAYA_HIP(hipStreamBeginCapture(E->stream, hipStreamCaptureModeThreadLocal));
+      hipGraph_t graph = nullptr;
+      try {
+        forward(*E, *s);
+      } catch (...) {
+        (void)hipStreamEndCapture(E->stream, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+      }
+      LAYA_HIP(hipStreamEndCapture(E->stream, &graph));
+      const hipError_t ie = hipGraphInstantiate(&s->graph, graph, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(graph);
+      LAYA_HIP(ie);
+    }
+    LAYA_HIP(hipEventRecord(s->start, E->stream));
+    if (capture && s->graph) {
+      LAYA_HIP(hipGraphLaunch(s->graph, E->stream));
+    } else {
+      forward(*E, *s);
+    }
+    LAYA_HIP(hipEventRecord(s->end, E->stream));
+    LAYA_HIP(hipMemcpyAsync(s->h_logits, s->logits, static_cast<size_t>(b) * (k + 1) * 4, hipMemcpyDeviceToHost, E->stream));
+    LAYA_HIP(hipMemcpyAsync(s->h_acts, s->acts, static_cast<size_t>(b) * E->cfg.n_act * 4, hipMemcpyDeviceToHost, E->stream));
+    LAYA_HIP(hipStreamSynchronize(E->stream));
+    float ms = 0.f;
+    LAYA_HIP(hipEventElapsedTime(&ms, s->start, s->end));
+    for (int q = 0; q < b; ++q)
+      std::memcpy(host_logits + static_cast<size_t>(q) * k, s->h_logits + static_cast<size_t>(q) * (k + 1) + 1, k * 4);
+    std::memcpy(host_acts, s->h_acts, static_cast<size_t>(b) * E->cfg.n_act * 4);
+    if (metrics) {
+      metrics->gpu_ms = ms;
+      metrics->cache_miss = miss;
+      metrics->graph_capture = captured_now;
+      metrics->graph_replay = capture && s->graph != nullptr;
+      metrics->owned_gpu_bytes = static_cast<int64_t>(E->weight_bytes + E->slot_bytes);
+    }
+  });
+}
+
+int laya_read_weight(void* handle, const char* name, float* host_out, int64_t count) {
+  Engine* E = static_cast<Engine*>(handle);
+  if (!E) return fail(nullptr, Failure{LAYA_EINVAL, "null handle"});
+  return guarded(E, [&] {
+    LAYA_REQUIRE(name && host_out, "null argument");
+    auto it = E->weights.find(name);
+    LAYA_REQUIRE(it != E->weights.end(), std::string("no resident tensor: ") + name);
+    const DevTensor& t = it->second;
+    LAYA_REQUIRE(static_cast<size_t>(count) == t.count, "element count mismatch");
+    LAYA_HIP(hipSetDevice(E->device));
+    if (t.dtype == DType::F32) {
+      LAYA_HIP(hipMemcpy(host_out, t.ptr, t.bytes, hipMemcpyDeviceToHost));
+    } else {
+      std::vector<uint16_t> raw(t.count);
+      LAYA_HIP(hipMemcpy(raw.data(), t.ptr, t.bytes, hipMemcpyDeviceToHost));
+      for (size_t i = 0; i < t.count; ++i)
+        host_out[i] = t.dtype == DType::BF16 ? bf16_bits_to_f32(raw[i]) : f16_bits_to_f32(raw[i]);
+    }
+  });
+}
+
+int64_t laya_used_bytes(void* handle) {
+  Engine* E = static_cast<Engine*>(handle);
+  return E ? static_cast<int64_t>(E->weight_bytes + E->slot_bytes) : 0;
+}
+
+int laya_slot_count(void* handle) {
+  Engine* E = static_cast<Engine*>(handle);
+  return E ? static_cast<int>(E->lru.size()) : 0;
+}
+
+int laya_destroy(void* handle) {
+  Engine* E = static_cast<Engine*>(handle);
+  if (!E) return LAYA_OK;
+  (void)hipSetDevice(E->device);
+  if (E->stream) (void)hipStreamSynchronize(E->stream);
+  for (Slot* s : E->lru) destroy_slot(*E, s);
+  E->lru.clear();
+  for (auto& kv : E->weights) (void)hipFree(kv.second.ptr);
+  E->weights.clear();
+  if (E->stream) (void)hipStreamDestroy(E->stream);
+  delete E;
+  return LAYA_OK;
+}
+
+const char* laya_last_error(void* handle) {
+  Engine* E = static_cast<Engine*>(handle);
+  return E ? E->error.c_str() : g_error.c_str();
+}
+
+// ---------------- kernel-level entry points ----------------
+
+int laya_attention_block(int waves) { return attention_block_rows(waves); }
+
+int laya_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_seq, int m, int block, int32_t* tiles,
+                         int max_tiles) {
+  int nt = 0, row = 0;
+  auto put = [&](int r0, int r1, int sq) {
+    if (nt >= max_tiles) return false;
+    tiles[3 * nt] = r0;
+    tiles[3 * nt + 1] = r1;
+    tiles[3 * nt + 2] = sq;
+    ++nt;
+    return true;
+  };
+  auto run = [&](int upto, int sq) {
+    while (row < upto) {
+      const int r1 = (upto - row > block) ? row + block : upto;
+      if (!put(row, r1, sq)) return false;
+      row = r1;
+    }
+    return true;
+  };
+  if (block <= 0 || block % 16) return -1;
+  for (int s = 0; s < n_seq; ++s) {
+    const int st = starts[s], e = st + span16(lengths[s]);
+    if (st % 16 || st < row || e > m) return -1;
+    if (!run(st, -1) || !run(e, s)) return -1;
+  }
+  if (!run(m, -1)) return -1;
+  return nt;
+}
+
+static DType half_type(int dtype16) { return dtype16 == LAYA_F16 ? DType::F16 : DType::BF16; }
+
+int laya_op_embed(const int32_t* ids, const int32_t* positions, const float* table, const float* pos_table,
+                  const float* type_row, const float* gamma, const float* beta, float eps, float* out32, void* out16,
+                  int dtype16, int rows, int width, int vocab, int n_positions, void* stream) {
+  return guarded(nullptr, [&] {
+    LAYA_REQUIRE(norm_width_supported(width), "unsupported width");
+    EmbedArgs a{ids, positions, table, pos_table, type_row, gamma, beta, eps, out32, out16, rows, vocab, n_positions};
+    check_launch(launch_embed(a, width, half_type(dtype16), static_cast<hipStream_t>(stream)), "embed");
+  });
+}
+
+int laya_op_norm(float* residual, const float* branch, int splits, int64_t part_stride, const float* bias,
+                 const float* gamma, const float* beta, float eps, float* sum_out, float* out32, void* out16,
+                 int dtype16, int rows, int width, void* stream) {
+  return guarded(nullptr, [&] {
+    LAYA_REQUIRE(norm_width_supported(width), "unsupported width");
+    AddNormArgs a{residual, branch, splits < 1 ? 1 : splits, part_stride, bias, gamma, beta, eps, sum_out, out32, out16, rows};
+    check_launch(launch_add_norm(a, width, half_type(dtype16), static_cast<hipStream_t>(stream)), "norm");
+  });
+}
+
+int laya_op_linear(const void* x, const void* w, const float* bias, void* out, int kind, int dtype16, int M, int N,
+                   int K, int splits, int tile, void* stream) {
+  return guarded(nullptr, [&] {
+    prepare_device();
+    LAYA_REQUIRE(kind >= 0 && kind <= 2, "kind must be 0 (fp32), 1 (16-bit) or 2 (16-bit GELU)");
+    const Epi epi = kind == 0 ? Epi::F32 : kind == 1 ? Epi::HALF : Epi::GELU;
+    int cus = 256;
+    if (tile < 0) {
+      gemm_plan(M, N, K, epi, cus, &tile, &splits);
+      if (bias) splits = 1;
+    }
+    LAYA_REQUIRE(tile < gemm_tile_count(), "bad tile id");
+    LAYA_REQUIRE(K % 64 == 0 && N % gemm_tile(tile).bn == 0, "K must be a multiple of 64 and N of the tile width");
+    GemmArgs g{};
+    g.a = x; g.b = w; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldb = K; g.bias = bias; g.out = out; g.ldo = N;
+    g.split_stride = static_cast<long long>(M) * N; g.splits = splits < 1 ? 1 : splits;
+    check_launch(launch_gemm(g, epi, half_type(dtype16), tile, static_cast<hipStream_t>(stream)), "linear");
+  });
+}
+
+int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* k, void* vt, int dtype16, int M,
+                int width, int tile, void* stream) {
+  return guarded(nullptr, [&] {
+    prepare_device();
+    int splits = 1;
+    if (tile < 0) gemm_plan(M, 3 * width, width, Epi::QKV, 256, &tile, &splits);
+    LAYA_REQUIRE(tile < gemm_tile_count(), "bad tile id");
+    LAYA_REQUIRE(width % 64 == 0 && (3 * width) % gemm_tile(tile).bn == 0, "width does not fit the tile");
+    GemmArgs g{};
+    g.a = x; g.b = w; g.M = M; g.N = 3 * width; g.K = width; g.lda = width; g.ldb = width; g.bias = bias;
+    g.splits = 1; g.q = q; g.k = k; g.vt = vt; g.width = width;
+    check_launch(launch_gemm(g, Epi::QKV, half_type(dtype16), tile, static_cast<hipStream_t>(stream)), "qkv");
+  });
+}
+
+int laya_op_attention(const void* q, const void* k, const void* vt, void* out, const int32_t* tiles,
+                      const int32_t* n_tiles, const int32_t* starts, const int32_t* lengths, int m, int heads,
+                      int max_tiles, int waves, int dtype16, void* stream) {
+  return guarded(nullptr, [&] {
+    LAYA_REQUIRE(waves == 1 || waves == 2 || waves == 4, "waves must be 1, 2 or 4");
+    AttnArgs a{q, k, vt, out, tiles, n_tiles, starts, lengths, m, heads, max_tiles};
+    check_launch(launch_attention(a, half_type(dtype16), waves, static_cast<hipStream_t>(stream)), "attention");
+  });
+}
+
+}  // extern "C"

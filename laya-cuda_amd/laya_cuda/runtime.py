@@ -1,0 +1,224 @@
+"""Runtime: resident weights and bounded shape slots, over liblaya_hip's C ABI.
+
+Same interface as the reference's Runtime (laya_cuda/runtime.py:136-197):
+``Runtime(adapter, device, max_cached_shapes)``, ``predict(items, capture=True) ->
+(logits, acts, metrics)``, ``close()``, ``weights[name]``, ``pool.used_bytes()``,
+``len(slots)``.  The device side - HBM arena, stream, one hipGraph per shape slot, LRU - is
+owned by the native library; this module validates checkpoints and packs requests.
+
+Packing follows Slot.fill (runtime.py:52-68): sequences back to back, each starting at a multiple
+of 16 rows; ``positions`` run 0..span-1 inside a sequence; ``rows`` is -1 past the last one;
+per question ``indices`` hold the absolute packed rows of its CLS token and option markers.
+Beyond the reference, several questions may share one sequence (``predict_sequences``):
+each question names its sequence, and its indices are offset by that sequence's start.
+"""
+import ctypes as ct
+
+import numpy as np
+
+from . import _lib
+
+
+def span(tokens):
+    """Rows start at multiples of 16 tokens, the attention tile."""
+    return -(-tokens // 16) * 16
+
+
+def _pow2(n, low):
+    return max(low, 1 << (n - 1).bit_length())
+
+
+def _round_rows(rows):
+    step = 32 if rows <= 256 else 64 if rows <= 512 else 128
+    return -(-rows // step) * step
+
+
+def classes(items):
+    """Shape class of reference-style items [(ids, markers, kind)]: one sequence per question."""
+    rows = sum(span(len(v[0])) for v in items)
+    return _round_rows(rows), _pow2(len(items), 1), _pow2(max(len(v[1]) for v in items), 8)
+
+
+def shape_class(sequences, questions):
+    """Shape class when questions share sequences: (rows, question capacity, option capacity)."""
+    rows = sum(span(len(ids)) for ids in sequences)
+    return (_round_rows(rows), _pow2(max(len(questions), len(sequences)), 1),
+            _pow2(max(len(q[1]) for q in questions), 8))
+
+
+def pack(sequences, questions, key, pad, vocab=None):
+    """Packed int32 block for liblaya_hip (field order in include/laya_hip.h)."""
+    m, b, k = key
+    size = 4 + 4 * m + 4 * b + b * (k + 1)
+    block = np.zeros(size, np.int32)
+    o = 4
+    ids, positions, rows, kinds = (block[o + i * m:o + (i + 1) * m] for i in range(4))
+    o += 4 * m
+    starts, lengths, counts, qkind = (block[o + i * b:o + (i + 1) * b] for i in range(4))
+    indices = block[o + 4 * b:].reshape(b, k + 1)
+    block[0], block[1] = len(sequences), len(questions)
+    ids.fill(pad)
+    rows.fill(-1)
+    first_kind = {}
+    for seq, _, kind in questions:
+        first_kind.setdefault(seq, kind)
+    offset = 0
+    for s, seq_ids in enumerate(sequences):
+        n = len(seq_ids)
+        end = offset + span(n)
+        ids[offset:offset + n] = seq_ids
+        positions[offset:end] = np.arange(end - offset, dtype=np.int32)
+        rows[offset:end] = s
+        kinds[offset:end] = first_kind.get(s, 0)
+        starts[s], lengths[s] = offset, n
+        offset = end
+    if offset > m:
+        raise ValueError("Packed sequences exceed the shape class")
+    for q, (s, markers, kind) in enumerate(questions):
+        if not 0 <= s < len(sequences):
+            raise ValueError(f"Question {q} names a missing sequence")
+        markers = np.asarray(markers, np.int64)
+        if len(markers) > k or (len(markers) and (markers.min() < 0 or markers.max() >= lengths[s])):
+            raise ValueError(f"Question {q} has option markers outside its sequence")
+        counts[q], qkind[q] = len(markers), kind
+        indices[q].fill(starts[s])
+        indices[q, 1:len(markers) + 1] += markers.astype(np.int32)
+    if vocab is not None and len(sequences) and (ids.min() < 0 or ids.max() >= vocab):
+        raise ValueError("Token id outside the vocabulary")
+    return block
+
+
+class _Resident:
+    """Read-back handle for a resident tensor (mirrors a CuPy array's ``.get()``)."""
+
+    def __init__(self, runtime, name, shape):
+        self.runtime, self.name, self.shape = runtime, name, tuple(shape)
+
+    def get(self):
+        out = np.empty(self.shape, np.float32)
+        ptr = out.ctypes.data_as(ct.POINTER(ct.c_float))
+        _lib.check(_lib.load().laya_read_weight(self.runtime._handle, self.name.encode(), ptr, out.size),
+                   self.runtime._handle)
+        return out
+
+
+class _Pool:
+    def __init__(self, runtime):
+        self.runtime = runtime
+
+    def used_bytes(self):
+        h = self.runtime._handle
+        return int(_lib.load().laya_used_bytes(h)) if h else 0
+
+    total_bytes = used_bytes
+
+
+class _Slots:
+    def __init__(self, runtime):
+        self.runtime = runtime
+
+    def __len__(self):
+        h = self.runtime._handle
+        return int(_lib.load().laya_slot_count(h)) if h else 0
+
+
+def _config(adapter):
+    precision = getattr(adapter, "mfma_dtype", "float16")
+    bert = getattr(adapter, "variant", "modernbert") == "bert"
+    return _lib.LayaConfig(
+        width=adapter.width, heads=adapter.heads, layers=adapter.layers, intermediate=adapter.intermediate,
+        vocab=adapter.vocab, max_positions=adapter.max_positions, type_vocab=adapter.type_vocab,
+        norm_order=_lib.NORM_POST if bert else _lib.NORM_PRE,
+        pos_kind=_lib.POS_LEARNED if bert else _lib.POS_ROPE,
+        ffn_kind=_lib.FFN_GELU if bert else _lib.FFN_GEGLU, bias=int(bert), eps=adapter.eps,
+        window=adapter.window if not bert else -1, global_every=adapter.global_every,
+        head_layers=adapter.head_layers, n_act=adapter.n_act, act_hidden=adapter.act_hidden,
+        max_len=adapter.max_len, mfma_dtype=_lib.F16 if precision == "float16" else _lib.BF16)
+
+
+def _host_dtype(array):
+    if array.dtype == np.float32:
+        return _lib.F32
+    if array.dtype == np.float16:
+        return _lib.F16
+    raise ValueError(f"Unsupported checkpoint dtype {array.dtype}")
+
+
+class Runtime:
+    """One engine on one HIP device: weights resident in HBM, shape slots with hipGraphs."""
+
+    def __init__(self, adapter, device, max_cached_shapes=16, *, weights=None):
+        self.adapter, self.device, self.limit = adapter, device, max_cached_shapes
+        self._handle = None
+        self.pool, self.slots = _Pool(self), _Slots(self)
+        self.weights = {}
+        lib = _lib.load()
+        handle = ct.c_void_p()
+        config = _config(adapter)
+        _lib.check(lib.laya_create(ct.byref(config), int(device), int(max_cached_shapes), ct.byref(handle)))
+        self._handle = handle
+        try:
+            shapes = adapter.weight_shapes()
+            if weights is None:
+                from safetensors import safe_open
+                with safe_open(str(adapter.path / "model.safetensors"), framework="numpy") as f:
+                    self._load(shapes, set(f.keys()), lambda n: tuple(f.get_slice(n).get_shape()), f.get_tensor)
+            else:
+                self._load(shapes, set(weights), lambda n: tuple(np.shape(weights[n])), lambda n: weights[n])
+            _lib.check(lib.laya_finalize(self._handle), self._handle)
+        except BaseException:
+            self.close()
+            raise
+
+    def _load(self, shapes, names, shape_of, tensor):
+        if names != set(shapes):
+            raise ValueError("Checkpoint tensor names do not match the Laya adapter")
+        for name, shape in shapes.items():
+            if shape_of(name) != tuple(shape):
+                raise ValueError(f"Incompatible tensor shape: {name}")
+        lib = _lib.load()
+        for name, shape in shapes.items():
+            if name == "temperature":
+                continue
+            array = np.ascontiguousarray(tensor(name))
+            if array.dtype not in (np.float32, np.float16):
+                array = array.astype(np.float32)
+            dims = (ct.c_int64 * len(shape))(*shape)
+            _lib.check(lib.laya_load_weight(self._handle, name.encode(), array.ctypes.data_as(ct.c_void_p),
+                                            _host_dtype(array), dims, len(shape)), self._handle)
+            self.weights[name] = _Resident(self, name, shape)
+
+    def predict(self, items, capture=True):
+        """Reference-style items [(ids, markers, kind)]: each question is its own sequence."""
+        sequences = [ids for ids, _, _ in items]
+        questions = [(i, markers, kind) for i, (_, markers, kind) in enumerate(items)]
+        return self.predict_sequences(sequences, questions, capture, key=classes(items))
+
+    def predict_sequences(self, sequences, questions, capture=True, key=None):
+        """Questions [(sequence index, markers, kind)] over shared sequences."""
+        if self._handle is None:
+            raise RuntimeError("Runtime is closed")
+        if not questions:
+            raise ValueError("Provide at least one question")
+        key = key or shape_class(sequences, questions)
+        block = pack(sequences, questions, key, self.adapter.pad, self.adapter.vocab)
+        m, b, k = key
+        logits = np.empty((b, k), np.float32)
+        acts = np.empty((b, self.adapter.n_act), np.float32)
+        shape = _lib.LayaShape(m, b, k)
+        metrics = _lib.LayaMetrics()
+        _lib.check(_lib.load().laya_predict(
+            self._handle, block.ctypes.data_as(ct.POINTER(ct.c_int32)), ct.byref(shape), int(bool(capture)),
+            logits.ctypes.data_as(ct.POINTER(ct.c_float)), acts.ctypes.data_as(ct.POINTER(ct.c_float)),
+            ct.byref(metrics)), self._handle)
+        n = len(questions)
+        return logits[:n], acts[:n], {
+            "gpu_ms": float(metrics.gpu_ms), "shape": key, "cache_miss": bool(metrics.cache_miss),
+            "graph_capture": bool(metrics.graph_capture), "graph_replay": bool(metrics.graph_replay),
+            "owned_gpu_bytes": int(metrics.owned_gpu_bytes)}
+
+    def close(self):
+        if self._handle is not None:
+            _lib.load().laya_destroy(self._handle)
+            self._handle = None
+        self.weights = {}

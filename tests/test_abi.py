@@ -1,0 +1,108 @@
+"""The C ABI library loads and exports every entry point include/laya_hip.h declares (no GPU)."""
+import ctypes as ct
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from laya_cuda import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "laya_hip.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|int64_t|const char\*)\s+(laya_\w+)\(", text, re.M)))
+
+
+def test_header_declares_the_boundary():
+    names = declared()
+    for name in ("laya_create", "laya_load_weight", "laya_finalize", "laya_predict", "laya_destroy",
+                 "laya_last_error", "laya_op_attention", "laya_op_linear"):
+        assert name in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    missing = [name for name in declared() if not hasattr(lib, name)]
+    assert not missing
+    assert set(declared()) <= set(_lib.SIGNATURES)
+    assert lib.laya_abi_version() == 1
+
+
+def test_packed_block_size_matches_the_python_packer():
+    from laya_cuda.runtime import pack
+    lib = _lib.load()
+    for m, b, k in [(96, 1, 8), (512, 2, 8), (16384, 128, 128)]:
+        shape = _lib.LayaShape(m, b, k)
+        seqs = [np.full(20, 7, np.int32)]
+        block = pack(seqs, [(0, [1, 2], 1)], (m, b, k), pad=0)
+        assert lib.laya_packed_ints(ct.byref(shape)) == block.size
+    assert lib.laya_packed_ints(ct.byref(_lib.LayaShape(0, 1, 8))) == -1
+
+
+def tiles(starts, lengths, m, block, max_tiles=None):
+    lib = _lib.load()
+    max_tiles = max_tiles or m // 16
+    out = np.zeros(3 * max_tiles, np.int32)
+    s, n = np.asarray(starts, np.int32), np.asarray(lengths, np.int32)
+    count = lib.laya_attention_tiles(s.ctypes.data_as(ct.POINTER(ct.c_int32)), n.ctypes.data_as(ct.POINTER(ct.c_int32)),
+                                     len(s), m, block, out.ctypes.data_as(ct.POINTER(ct.c_int32)), max_tiles)
+    return count, out[:3 * max(count, 0)].reshape(-1, 3)
+
+
+@pytest.mark.parametrize("block", [32, 64, 128])
+def test_attention_tiles_cover_every_row_once(block):
+    lengths = [250, 131, 1, 16, 500]
+    starts, at = [], 0
+    for n in lengths:
+        starts.append(at)
+        at += -(-n // 16) * 16
+    m = at + 64
+    count, t = tiles(starts, lengths, m, block)
+    assert count > 0
+    covered = np.zeros(m, int)
+    for r0, r1, seq in t:
+        assert 0 < r1 - r0 <= block
+        covered[r0:r1] += 1
+        if seq >= 0:  # a tile never straddles a sequence's span
+            assert starts[seq] <= r0 and r1 <= starts[seq] + -(-lengths[seq] // 16) * 16
+    assert (covered == 1).all()
+    assert (t[:, 2] == -1).sum() >= 1  # rows past the last sequence are zero tiles
+
+
+def test_attention_tiles_reject_bad_layouts():
+    assert tiles([8], [10], 64, 64)[0] == -1            # not 16-aligned
+    assert tiles([0, 0], [16, 16], 64, 64)[0] == -1     # overlapping
+    assert tiles([0], [100], 64, 64)[0] == -1           # past the slot
+    assert tiles([0], [64], 64, 16, max_tiles=2)[0] == -1  # tile list too small
+
+
+def test_create_without_gpu_reports_an_error():
+    """On a machine without a usable gfx950 device, create fails with a message, not a crash."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    lib = _lib.load()
+    cfg = _lib.LayaConfig(width=64, heads=1, layers=1, intermediate=256, vocab=10, max_positions=16, type_vocab=2,
+                          norm_order=0, pos_kind=0, ffn_kind=0, bias=1, eps=1e-12, window=-1, global_every=1,
+                          head_layers=0, n_act=2, act_hidden=256, max_len=16, mfma_dtype=_lib.F16)
+    handle = ct.c_void_p()
+    rc = lib.laya_create(ct.byref(cfg), 0, 4, ct.byref(handle))
+    assert rc != 0 and not handle.value
+    assert _lib.error(None)
+
+
+def test_create_rejects_unbuilt_variants_before_touching_the_device():
+    lib = _lib.load()
+    cfg = _lib.LayaConfig(width=64, heads=1, layers=1, intermediate=256, vocab=10, max_positions=16, type_vocab=2,
+                          norm_order=1, pos_kind=1, ffn_kind=1, bias=0, eps=1e-5, window=64, global_every=3,
+                          head_layers=1, n_act=2, act_hidden=256, max_len=16, mfma_dtype=_lib.F16)
+    handle = ct.c_void_p()
+    assert lib.laya_create(ct.byref(cfg), 0, 4, ct.byref(handle)) == _lib.EINVAL
+    assert "variant not built" in _lib.error(None)
+    cfg.norm_order, cfg.pos_kind, cfg.ffn_kind, cfg.bias, cfg.window, cfg.head_layers = 0, 0, 0, 1, -1, 0
+    cfg.heads = 2  # width != heads * 64
+    assert lib.laya_create(ct.byref(cfg), 0, 4, ct.byref(handle)) == _lib.EINVAL
+    assert "64-wide" in _lib.error(None)

@@ -1,0 +1,295 @@
+"""Kernel-level parity on the GPU, through the C ABI (laya_op_*), against NumPy oracles.
+
+Mirrors the reference's kernel tests (tests/test_gpu.py, tests/test_attention.py): bit-exact
+gathers and residual adds, bias-before-rounding, LayerNorm and GEMM tolerances, packed ragged
+attention with padding rows returning exact zeros.  Device memory comes from torch (plumbing
+only); every computation runs in liblaya_hip.
+"""
+import ctypes as ct
+import math
+
+import numpy as np
+import pytest
+
+import oracle.encoder as E
+from laya_cuda import _lib
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"f16": (_lib.F16, np.float16), "bf16": (_lib.BF16, None)}
+
+
+def torch():
+    import torch as t
+    return t
+
+
+def dev(array, device):
+    t = torch()
+    return t.from_numpy(np.ascontiguousarray(array)).to(device)
+
+
+def p(tensor):
+    return ct.c_void_p(tensor.data_ptr()) if tensor is not None else None
+
+
+def stream():
+    return ct.c_void_p(torch().cuda.current_stream().cuda_stream)
+
+
+def sync():
+    torch().cuda.synchronize()
+
+
+def half_round(a, kind):
+    """Round float32 values to the 16-bit operand type, as float32."""
+    from laya_cuda.synthetic import bf16_round
+    a = np.asarray(a, np.float32)
+    return a.astype(np.float16).astype(np.float32) if kind == "f16" else bf16_round(a)
+
+
+def to16(a, kind, device):
+    t = torch()
+    x = dev(half_round(a, kind), device)
+    return x.to(t.float16 if kind == "f16" else t.bfloat16)
+
+
+def from16(x):
+    return x.float().cpu().numpy()
+
+
+def check(code):
+    _lib.check(code)
+
+
+# ---------------- embedding gather + LayerNorm ----------------
+
+def test_embed_gather_is_bit_exact(gpu):
+    t = torch()
+    lib = _lib.load()
+    rng = np.random.default_rng(1)
+    table = rng.normal(0, 1, (1000, 768)).astype(np.float32)
+    pos = rng.normal(0, 1, (64, 768)).astype(np.float32)
+    typ = rng.normal(0, 1, (2, 768)).astype(np.float32)
+    ids = np.array([0, 999, 3, 3, 17, 500, 3, 999], np.int32)
+    positions = np.array([0, 1, 2, 3, 63, 5, 6, 0], np.int32)
+    d_ids, d_pos, d_table, d_ptab, d_type = (dev(a, gpu) for a in (ids, positions, table, pos, typ))
+    out = t.full((len(ids), 768), float("nan"), device=gpu)
+    check(lib.laya_op_embed(p(d_ids), p(d_pos), p(d_table), None, None, None, None, 0.0, p(out), None, _lib.F16,
+                            len(ids), 768, 1000, 64, stream()))
+    sync()
+    np.testing.assert_array_equal(out.cpu().numpy(), table[ids])
+    check(lib.laya_op_embed(p(d_ids), p(d_pos), p(d_table), p(d_ptab), p(d_type), None, None, 0.0, p(out), None,
+                            _lib.F16, len(ids), 768, 1000, 64, stream()))
+    sync()
+    np.testing.assert_array_equal(out.cpu().numpy(), (table[ids] + pos[positions]) + typ[0])
+
+
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+@pytest.mark.parametrize("width", [128, 768, 1024])
+def test_embed_norm_matches_oracle(gpu, kind, width):
+    t = torch()
+    lib = _lib.load()
+    rng = np.random.default_rng(width)
+    table = rng.normal(0, .5, (300, width)).astype(np.float32)
+    pos = rng.normal(0, .5, (128, width)).astype(np.float32)
+    typ = rng.normal(0, .5, (2, width)).astype(np.float32)
+    gamma, beta = rng.normal(1, .1, width).astype(np.float32), rng.normal(0, .1, width).astype(np.float32)
+    ids = rng.integers(0, 300, 77).astype(np.int32)
+    positions = np.arange(77, dtype=np.int32)
+    out32 = t.full((77, width), float("nan"), device=gpu)
+    out16 = t.empty((77, width), dtype=t.float16 if kind == "f16" else t.bfloat16, device=gpu)
+    args = [dev(a, gpu) for a in (ids, positions, table, pos, typ, gamma, beta)]
+    check(lib.laya_op_embed(*[p(a) for a in args], 1e-12, p(out32), p(out16), DTYPES[kind][0], 77, width, 300, 128,
+                            stream()))
+    sync()
+    expected = E.layer_norm((table[ids] + pos[positions]) + typ[0], gamma, beta, 1e-12)
+    np.testing.assert_allclose(out32.cpu().numpy(), expected, atol=2e-5, rtol=1e-5)
+    np.testing.assert_array_equal(from16(out16), half_round(out32.cpu().numpy(), kind))
+
+
+# ---------------- residual add + LayerNorm ----------------
+
+@pytest.mark.parametrize("width", [64, 768, 1024, 1088])
+@pytest.mark.parametrize("normalize,out32", [(False, False), (False, True), (True, False), (True, True)])
+def test_norm_residual_and_aliases(gpu, width, normalize, out32):
+    """tests/test_gpu.py:79-103 of the reference: residual add bit-exact, LN within tolerance,
+    fp32 output aliasing the residual (in-place post-LN)."""
+    t = torch()
+    lib = _lib.load()
+    rng = np.random.default_rng(31)
+    source = rng.normal(2, .3, (3, width)).astype(np.float32)
+    branch = rng.normal(0, .1, (3, width)).astype(np.float32)
+    gamma, beta = rng.normal(1, .1, width).astype(np.float32), rng.normal(0, .1, width).astype(np.float32)
+    residual, d_branch, d_g, d_b = (dev(a, gpu) for a in (source, branch, gamma, beta))
+    added = source + branch
+    if out32:
+        out, out16, sum_out = residual, None, None
+    else:
+        out, out16, sum_out = None, t.empty((3, width), dtype=t.float16, device=gpu), residual
+    check(lib.laya_op_norm(p(residual), p(d_branch), 1, 0, None, p(d_g) if normalize else None,
+                           p(d_b) if normalize else None, 1e-5, p(sum_out), p(out), p(out16), _lib.F16, 3, width,
+                           stream()))
+    sync()
+    got = residual.cpu().numpy() if out32 else from16(out16)
+    if normalize:
+        a64 = added.astype(np.float64)
+        expected = (a64 - a64.mean(-1, keepdims=True)) / np.sqrt(a64.var(-1, keepdims=True) + 1e-5) * gamma + beta
+        np.testing.assert_allclose(got, expected, atol=2e-5 if out32 else 4e-3, rtol=1e-5 if out32 else 2e-3)
+    else:
+        np.testing.assert_array_equal(got, added if out32 else added.astype(np.float16).astype(np.float32))
+    if not out32:
+        np.testing.assert_array_equal(residual.cpu().numpy(), added)
+
+
+def test_norm_sums_split_partials_and_bias_in_order(gpu):
+    lib = _lib.load()
+    rng = np.random.default_rng(2)
+    rows, width, splits = 5, 768, 3
+    res = rng.normal(0, 1, (rows, width)).astype(np.float32)
+    parts = rng.normal(0, 1, (splits, rows, width)).astype(np.float32)
+    bias = rng.normal(0, 1, width).astype(np.float32)
+    d_res, d_parts, d_bias = (dev(a, gpu) for a in (res, parts, bias))
+    check(lib.laya_op_norm(p(d_res), p(d_parts), splits, rows * width, p(d_bias), None, None, 1e-5, None, p(d_res),
+                           None, _lib.F16, rows, width, stream()))
+    sync()
+    np.testing.assert_array_equal(d_res.cpu().numpy(), res + (((parts[0] + parts[1]) + parts[2]) + bias))
+
+
+# ---------------- MFMA GEMM ----------------
+
+def linear(x, w, bias, out, kind, dtype, M, N, K, splits, tile):
+    check(_lib.load().laya_op_linear(p(x), p(w), p(bias), p(out), kind, DTYPES[dtype][0], M, N, K, splits, tile,
+                                     stream()))
+    sync()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("tile", range(7))
+def test_linear_tiles_match_fp32_product(gpu, dtype, tile):
+    t = torch()
+    rng = np.random.default_rng(tile)
+    for M, N, K in [(96, 768, 768), (300, 512, 1024), (512, 256, 128)]:
+        x = half_round(rng.normal(0, 1, (M, K)), dtype)
+        w = half_round(rng.normal(0, 1 / math.sqrt(K), (N, K)), dtype)
+        out = t.full((M, N), float("nan"), device=gpu)
+        linear(to16(x, dtype, gpu), to16(w, dtype, gpu), None, out, 0, dtype, M, N, K, 1, tile)
+        np.testing.assert_allclose(out.cpu().numpy(), x.astype(np.float64) @ w.T.astype(np.float64),
+                                   atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("splits", [2, 3, 4])
+def test_linear_split_k_partials_sum_to_the_product(gpu, splits):
+    t = torch()
+    rng = np.random.default_rng(splits)
+    M, N, K = 64, 768, 3072
+    x = half_round(rng.normal(0, 1, (M, K)), "f16")
+    w = half_round(rng.normal(0, 1 / math.sqrt(K), (N, K)), "f16")
+    out = t.full((splits, M, N), float("nan"), device=gpu)
+    linear(to16(x, "f16", gpu), to16(w, "f16", gpu), None, out, 0, "f16", M, N, K, splits, 5)
+    np.testing.assert_allclose(out.sum(0).cpu().numpy(), x.astype(np.float64) @ w.T.astype(np.float64),
+                               atol=1e-4, rtol=1e-4)
+
+
+def test_linear_adds_bias_before_rounding(gpu):
+    """tests/test_gpu.py:56-65 of the reference: (x w^T + b) rounded once."""
+    t = torch()
+    x = np.zeros((1, 64), np.float32)
+    x[0, :2] = [1, .0006]
+    w = np.ones((128, 64), np.float32)
+    bias = np.full(128, -1, np.float32)
+    out = t.empty((1, 128), dtype=t.float16, device=gpu)
+    linear(to16(x, "f16", gpu), to16(w, "f16", gpu), dev(bias, gpu), out, 1, "f16", 1, 128, 64, 1, 6)
+    x16 = x.astype(np.float16).astype(np.float32)
+    oracle = (x16 @ w.T + bias).astype(np.float16)
+    np.testing.assert_array_equal(out.cpu().numpy(), oracle)
+    assert oracle[0, 0] != 0  # rounding before the bias would give exactly zero
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_linear_gelu_epilogue(gpu, dtype):
+    t = torch()
+    rng = np.random.default_rng(9)
+    M, N, K = 128, 3072, 768
+    x = half_round(rng.normal(0, 1, (M, K)), dtype)
+    w = half_round(rng.normal(0, 2 / math.sqrt(K), (N, K)), dtype)
+    bias = rng.normal(0, .5, N).astype(np.float32)
+    out = t.empty((M, N), dtype=t.float16 if dtype == "f16" else t.bfloat16, device=gpu)
+    linear(to16(x, dtype, gpu), to16(w, dtype, gpu), dev(bias, gpu), out, 2, dtype, M, N, K, 1, -1)
+    expected = E.gelu((x.astype(np.float64) @ w.T.astype(np.float64) + bias).astype(np.float32))
+    tol = 2e-3 if dtype == "f16" else 1e-2
+    np.testing.assert_allclose(from16(out), expected, atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("tile", [0, 2, 5, 6])
+def test_qkv_epilogue_writes_head_major_layout(gpu, tile):
+    """Integer-valued operands make the product exact, so the layout check is bit-exact."""
+    t = torch()
+    rng = np.random.default_rng(tile)
+    M, heads = 96, 4
+    width = heads * 64
+    x = rng.integers(-3, 4, (M, width)).astype(np.float32)
+    w = rng.integers(-2, 3, (3 * width, width)).astype(np.float32)
+    bias = rng.integers(-4, 5, 3 * width).astype(np.float32)
+    q, k, vt = (t.full((heads * M * 64,), float("nan"), dtype=t.float16, device=gpu) for _ in range(3))
+    check(_lib.load().laya_op_qkv(p(to16(x, "f16", gpu)), p(to16(w, "f16", gpu)), p(dev(bias, gpu)), p(q), p(k),
+                                  p(vt), _lib.F16, M, width, tile, stream()))
+    sync()
+    full = x @ w.T + bias  # [M, 3*width], exact in fp32 and fp16
+    parts = full.reshape(M, 3, heads, 64)
+    np.testing.assert_array_equal(q.cpu().numpy().reshape(heads, M, 64), parts[:, 0].transpose(1, 0, 2))
+    np.testing.assert_array_equal(k.cpu().numpy().reshape(heads, M, 64), parts[:, 1].transpose(1, 0, 2))
+    np.testing.assert_array_equal(vt.cpu().numpy().reshape(heads, 64, M), parts[:, 2].transpose(1, 2, 0))
+
+
+# ---------------- fused attention ----------------
+
+def span(n):
+    return -(-n // 16) * 16
+
+
+@pytest.mark.parametrize("waves", [1, 2, 4])
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("lengths", [[32], [7, 96], [128, 1], [250, 131], [256, 219, 145], [500], [1024, 333]])
+def test_packed_attention_matches_float64(gpu, lengths, dtype, waves):
+    """tests/test_attention.py:12-56 of the reference (window -1): ragged packed rows, tokens past
+    the last row, NaN-poisoned output, padding queries exactly zero."""
+    t = torch()
+    lib = _lib.load()
+    h = 2
+    starts = np.cumsum([0] + [span(n) for n in lengths])[:-1].astype(np.int32)
+    m = span(sum(span(n) for n in lengths) + 16)
+    x = half_round(np.random.default_rng(m).normal(0, 1, (m, 3, h, 64)), dtype)
+    q = x[:, 0].transpose(1, 0, 2).copy()              # [h][m][64]
+    k = x[:, 1].transpose(1, 0, 2).copy()
+    vt = x[:, 2].transpose(1, 2, 0).copy()             # [h][64][m]
+    max_tiles = m // 16
+    block = lib.laya_attention_block(waves)
+    tiles = np.zeros(3 * max_tiles, np.int32)
+    lens = np.asarray(lengths, np.int32)
+    n = lib.laya_attention_tiles(starts.ctypes.data_as(ct.POINTER(ct.c_int32)), lens.ctypes.data_as(ct.POINTER(ct.c_int32)),
+                                 len(lengths), m, block, tiles.ctypes.data_as(ct.POINTER(ct.c_int32)), max_tiles)
+    assert n > 0
+    out = t.full((m, h * 64), float("nan"), dtype=t.float16 if dtype == "f16" else t.bfloat16, device=gpu)
+    args = [to16(a, dtype, gpu) for a in (q, k, vt)] + [out] + [dev(a, gpu) for a in (tiles, np.array([n], np.int32),
+                                                                                       starts, lens)]
+
+    def run():
+        check(lib.laya_op_attention(*[p(a) for a in args], m, h, max_tiles, waves, DTYPES[dtype][0], stream()))
+        sync()
+        return from16(out)
+
+    eager = run()
+    out.fill_(float("nan"))
+    np.testing.assert_array_equal(run(), eager)  # deterministic
+    real = np.zeros(m, bool)
+    atol, rtol = (6e-4, 1e-3) if dtype == "f16" else (4e-3, 8e-3)
+    for start, n_tok in zip(starts, lengths):
+        real[start:start + n_tok] = True
+        qq, kk, vv = x[start:start + n_tok].astype(np.float64).transpose(1, 2, 0, 3)
+        s = qq @ kk.transpose(0, 2, 1) / 8
+        pr = np.exp(s - s.max(-1, keepdims=True))
+        pr /= pr.sum(-1, keepdims=True)
+        expected = (pr @ vv).transpose(1, 0, 2).reshape(n_tok, h * 64)
+        np.testing.assert_allclose(eager[start:start + n_tok], expected, atol=atol, rtol=rtol)
+    np.testing.assert_array_equal(eager[~real], 0)

@@ -1,0 +1,167 @@
+"""End-to-end parity of the HIP encoder path against the CPU oracle, and slot/graph lifecycle.
+
+Bar (north star): bit-exact gathers (kernel tests), max |logit - oracle| <= 1e-3 with fp32
+accumulation and identical argmax decisions; graph replays bit-equal to eager passes.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle.encoder as E
+from laya_cuda import synthetic
+from laya_cuda.runtime import Runtime
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+LOGIT_ATOL = 1e-3
+
+
+def _cfg(spec):
+    return {"width": spec.width, "heads": spec.heads, "eps": spec.eps, "layers": spec.layers}
+
+
+def oracle_logits(spec, w, sequences, questions):
+    logits, acts, _ = E.forward(sequences, questions, E.structured(w, _cfg(spec)), _cfg(spec))
+    return logits, acts
+
+
+def compare(got_logits, got_acts, want_logits, want_acts, atol=LOGIT_ATOL):
+    worst = 0.0
+    for q, want in enumerate(want_logits):
+        got = got_logits[q, :len(want)]
+        worst = max(worst, float(np.abs(got - want).max()))
+        assert np.argmax(got) == np.argmax(want), f"question {q}: decision differs"
+    assert worst <= atol, f"max |logit error| {worst:.3e} > {atol}"
+    np.testing.assert_allclose(got_acts, want_acts, atol=atol)
+    return worst
+
+
+def test_small_encoder_matches_golden_and_oracle(gpu):
+    spec = synthetic.adapter(None, layers=2, width=128, heads=2, intermediate=512, vocab=1000, positions=64,
+                             max_len=64)
+    g = np.load(GOLDEN / "bert_small.npz")
+    w = synthetic.weights(spec, seed=int(g["seed"]), random_norms=True, std=float(g["std"]))
+    sequences = [g[f"ids{s}"] for s in range(int(g["n_seq"]))]
+    questions = [(int(g[f"q{q}_seq"]), list(g[f"q{q}_markers"]), int(g[f"q{q}_kind"])) for q in range(int(g["n_q"]))]
+    rt = Runtime(spec, 0, 4, weights=w)
+    try:
+        logits, acts, metrics = rt.predict_sequences(sequences, questions)
+        golden = [g[f"q{q}_logits"] for q in range(len(questions))]
+        compare(logits, acts, golden, np.stack([g[f"q{q}_acts"] for q in range(len(questions))]), atol=5e-3)
+        want, want_acts = oracle_logits(spec, w, sequences, questions)
+        compare(logits, acts, want, want_acts, atol=5e-3)
+        assert metrics["cache_miss"] and metrics["graph_capture"] and metrics["graph_replay"]
+    finally:
+        rt.close()
+
+
+@pytest.mark.parametrize("name", ["l83", "l512"])
+def test_workload_matches_oracle(gpu, name):
+    spec = synthetic.adapter(name)
+    w = synthetic.weights(spec, seed=0)
+    sequences, questions = synthetic.request(name, seed=1)
+    want, want_acts = oracle_logits(spec, w, sequences, questions)
+    rt = Runtime(spec, 0, 4, weights=w)
+    try:
+        logits, acts, _ = rt.predict_sequences(sequences, questions)
+        worst = compare(logits, acts, want, want_acts)
+        print(f"{name}: max |logit error| = {worst:.3e}")
+        eager = rt.predict_sequences(sequences, questions, capture=False)
+        np.testing.assert_array_equal(eager[0], logits)
+        np.testing.assert_array_equal(eager[1], acts)
+    finally:
+        rt.close()
+
+
+def test_ragged_batch_matches_oracle(gpu):
+    spec = synthetic.adapter("ragged32")
+    w = synthetic.weights(spec, seed=0)
+    sequences, questions = synthetic.request("ragged32", seed=1)
+    want, want_acts = oracle_logits(spec, w, sequences, questions)
+    rt = Runtime(spec, 0, 4, weights=w)
+    try:
+        logits, acts, metrics = rt.predict_sequences(sequences, questions)
+        worst = compare(logits, acts, want, want_acts)
+        print(f"ragged32: {len(questions)} questions, max |logit error| = {worst:.3e}, shape {metrics['shape']}")
+    finally:
+        rt.close()
+
+
+def test_reference_items_each_question_its_own_row(gpu):
+    """Runtime.predict(items) packs every question as its own sequence (runtime.py:52-68)."""
+    spec = synthetic.adapter(None, layers=2, width=128, heads=2, intermediate=512, vocab=1000, positions=64,
+                             max_len=64)
+    w = synthetic.weights(spec, seed=7)
+    rng = np.random.default_rng(8)
+    items = [(list(rng.integers(5, 1000, n)), sorted(rng.choice(np.arange(1, n), c, replace=False).tolist()), kind)
+             for n, c, kind in [(20, 3, 0), (50, 2, 1), (9, 1, 2)]]
+    rt = Runtime(spec, 0, 4, weights=w)
+    try:
+        logits, acts, metrics = rt.predict(items)
+        assert metrics["shape"] == (128, 4, 8)
+        want, want_acts = oracle_logits(spec, w, [i[0] for i in items], [(q, i[1], i[2]) for q, i in enumerate(items)])
+        compare(logits, acts, want, want_acts)
+    finally:
+        rt.close()
+
+
+def test_slot_lifecycle_graph_replay_and_eviction(gpu):
+    """tests/test_runtime.py:13-53 of the reference, on a synthetic checkpoint."""
+    spec = synthetic.adapter(None, layers=2, width=128, heads=2, intermediate=512, vocab=1000, positions=64,
+                             max_len=64)
+    w = synthetic.weights(spec, seed=11)
+    rng = np.random.default_rng(12)
+    short = [(list(rng.integers(5, 1000, 12)), [1, 2], 0)]
+    long = [(list(rng.integers(5, 1000, 60)), [5, 9, 30], 0)]
+    other = [(list(rng.integers(5, 1000, 12)), [3, 4], 0)]
+    rt = Runtime(spec, 0, 1, weights=w)
+    try:
+        first = rt.predict(short)
+        assert first[2]["cache_miss"] and first[2]["graph_capture"] and first[2]["graph_replay"]
+        again = rt.predict(short)
+        assert not again[2]["cache_miss"] and not again[2]["graph_capture"] and again[2]["graph_replay"]
+        np.testing.assert_array_equal(first[0], again[0])
+        raw = rt.predict(short, capture=False)
+        np.testing.assert_array_equal(raw[0], first[0])
+        np.testing.assert_array_equal(raw[1], first[1])
+        # reusing one graph must upload new contents, not return the previous answer
+        changed = rt.predict(other)
+        assert not np.array_equal(changed[0], first[0])
+        np.testing.assert_array_equal(rt.predict(other, capture=False)[0], changed[0])
+        rt.predict(long)
+        assert len(rt.slots) == 1
+        back = rt.predict(short)
+        assert back[2]["cache_miss"] and back[2]["graph_capture"]
+        np.testing.assert_array_equal(back[0], first[0])
+        assert rt.pool.used_bytes() > 0
+        np.testing.assert_array_equal(rt.weights["act_head.2.bias"].get(), w["act_head.2.bias"])
+    finally:
+        rt.close()
+    assert rt.pool.used_bytes() == 0
+    with pytest.raises(RuntimeError, match="closed"):
+        rt.predict(short)
+
+
+def test_changed_weights_change_the_answer(gpu):
+    """tests/test_custom_models.py:14-57: zero weights, the act probability follows the bias."""
+    spec = synthetic.adapter(None, layers=1, width=64, heads=1, intermediate=256, vocab=100, positions=64,
+                             max_len=64)
+    weights = {name: np.zeros(shape, np.float32) for name, shape in spec.weight_shapes().items()}
+    for name in weights:
+        if "norm" in name and name.endswith("weight") or name == "scorer.0.weight":
+            weights[name][:] = 1
+    probs = []
+    for bias in ([-4, 4], [4, -4]):
+        weights["act_head.2.bias"] = np.array(bias, np.float32)
+        rt = Runtime(spec, 0, 2, weights=weights)
+        try:
+            _, acts, _ = rt.predict([([1, 2, 3, 4], [1, 2], 0)])
+            e = np.exp(acts[0] - acts[0].max())
+            probs.append(e[0] / e.sum())
+        finally:
+            rt.close()
+    assert probs[0] < .001 and probs[1] > .999
+    weights["act_head.2.bias"] = np.zeros(3, np.float32)
+    with pytest.raises(ValueError, match="Incompatible tensor shape"):
+        Runtime(spec, 0, 2, weights=weights)
