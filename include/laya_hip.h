@@ -111,6 +111,20 @@ int laya_finalize(void* handle);
 int laya_predict(void* handle, const int32_t* host_packed, const LayaShape* shape, int capture,
                  float* host_logits, float* host_acts, LayaMetrics* metrics);
 
+/* Per-launch timing, the native counterpart of the reference's profiling hook that records events
+ * around every Ops.call/linear (tools/profile_long.py:21-67).  The forward is a fixed list of
+ * stages (embed_norm; per layer qkv, attention, attn_out, attn_norm, ffn_up, ffn_down, ffn_norm;
+ * head_gather, head_scorer, head_finish).  laya_time_stage uploads the request like
+ * laya_predict, runs one eager forward so every buffer holds this request's values, then launches
+ * stage `stage` of layer `layer` `reps` times back to back between two events on the engine's
+ * stream and stores the average per launch in *avg_ms.  Stages that normalise in place
+ * (attn_norm, ffn_norm) change the residual on every repetition: time them, do not read results
+ * afterwards. */
+int laya_stage_count(void);
+const char* laya_stage_name(int stage);
+int laya_time_stage(void* handle, const int32_t* host_packed, const LayaShape* shape, int stage, int layer,
+                    int reps, float* avg_ms);
+
 /* Read a resident tensor back as fp32 (runtime.weights[name], tests/test_custom_models.py:46). */
 int laya_read_weight(void* handle, const char* name, float* host_out, int64_t count);
 int64_t laya_used_bytes(void* handle);   /* weights + slots: CuPy pool used_bytes() */

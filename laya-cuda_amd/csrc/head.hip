@@ -9,7 +9,9 @@
 //
 // Only the head rows that exist are computed: the host lists them compactly (question by
 // question: CLS, then each option), so a slot whose option capacity is padded to a power of two
-// does no work for the padding.
+// does no work for the padding.  Launches: gather+LN, scorer.1 (fp32 MFMA, split-K), scorer tail
+// (a wave per row), features (a workgroup per question), act_head.0 (the same fp32 MFMA GEMM over
+// all questions, K padded with zeros to a multiple of 256 so it splits 8-16 ways), act output.
 #include "kernels.hpp"
 #include "rowops.hpp"
 
@@ -80,95 +82,98 @@ __global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
     }
 }
 
-// One workgroup per question: logits of its CLS + option rows, softmax features, act head.
+// Scorer tail, one wave per compact head row (CLS or option): logit = w3 . gelu(v + b1) + b3.
 template <int D>
-__global__ __launch_bounds__(256) void head_finish_kernel(HeadFinishArgs a) {
-  const int q = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float* logits = a.logits + static_cast<size_t>(q) * (a.k + 1);
-  float* acts = a.acts + static_cast<size_t>(q) * a.n_act;
-  if (q >= *a.n_q) {  // unused question slots of the shape class
-    for (int j = tid; j <= a.k; j += 256) logits[j] = 0.f;
-    for (int j = tid; j < a.n_act; j += 256) acts[j] = 0.f;
-    return;
+__global__ __launch_bounds__(256) void head_logit_kernel(HeadLogitArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.cap || r >= *a.n_sel) return;
+  const size_t off = static_cast<size_t>(r) * D;
+  float v[D / 64], t[D / 64];
+  load_row<D>(a.parts + off, lane, v);
+  for (int s = 1; s < a.splits; ++s) {
+    load_row<D>(a.parts + s * a.split_stride + off, lane, t);
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) v[i] = v[i] + t[i];
   }
-  extern __shared__ float sh[];
-  float* slog = sh;                 // [k+1]
-  float* feat = slog + (a.k + 1);   // [D+4]
-  float* hid = feat + (D + 4);      // [hidden]
-  const int count = a.counts[q], base = a.qoff[q];
-
   float b1[D / 64], w3[D / 64];
   load_row<D>(a.b1, lane, b1);
   load_row<D>(a.w3, lane, w3);
-  for (int j = wave; j <= a.k; j += 4) {
-    float logit = 0.f;
-    if (j <= count) {
-      const size_t off = static_cast<size_t>(base + j) * D;
-      float v[D / 64];
-      load_row<D>(a.parts + off, lane, v);
-      for (int s = 1; s < a.splits; ++s) {
-        float t[D / 64];
-        load_row<D>(a.parts + s * a.split_stride + off, lane, t);
+  float dot = 0.f;
 #pragma unroll
-        for (int i = 0; i < D / 64; ++i) v[i] = v[i] + t[i];
-      }
-      float dot = 0.f;
-#pragma unroll
-      for (int i = 0; i < D / 64; ++i) dot += gelu(v[i] + b1[i]) * w3[i];
-      logit = wave_sum(dot) + a.b3[0];
-    }
-    if (lane == 0) {
-      logits[j] = logit;
-      slog[j] = logit;
+  for (int i = 0; i < D / 64; ++i) dot += gelu(v[i] + b1[i]) * w3[i];
+  const float logit = wave_sum(dot) + a.b3[0];
+  if (lane == 0) {
+    const int q = a.sel_q[r];
+    a.row_logit[r] = logit;
+    a.logits[static_cast<size_t>(q) * (a.k + 1) + (r - a.qoff[q])] = logit;
+  }
+}
+
+// One workgroup per question slot: softmax statistics over its option logits (slots 1..count),
+// written with its CLS row as the act head's input row (zero-padded to kp columns).
+__global__ __launch_bounds__(256) void head_features_kernel(HeadFeatureArgs a) {
+  const int q = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float* logits = a.logits + static_cast<size_t>(q) * (a.k + 1);
+  float* feat = a.feat + static_cast<size_t>(q) * a.kp;
+  if (q >= *a.n_q) {  // unused question slots of the shape class
+    for (int j = tid; j <= a.k; j += 256) logits[j] = 0.f;
+    for (int j = tid; j < a.kp; j += 256) feat[j] = 0.f;
+    for (int j = tid; j < a.n_act; j += 256) a.acts[static_cast<size_t>(q) * a.n_act + j] = 0.f;
+    return;
+  }
+  const int count = a.counts[q], base = a.qoff[q];
+  for (int j = count + 1 + tid; j <= a.k; j += 256) logits[j] = 0.f;
+  for (int e = tid; e < a.width; e += 256) feat[e] = a.selected[static_cast<size_t>(base) * a.width + e];
+  for (int e = a.width + 4 + tid; e < a.kp; e += 256) feat[e] = 0.f;
+  if (wave != 0) return;
+  const float* z = a.row_logit + base + 1;
+  float mx = -INFINITY;
+  for (int j = lane; j < count; j += 64) mx = fmaxf(mx, z[j]);
+  mx = wave_max(mx);
+  float se = 0.f;
+  for (int j = lane; j < count; j += 64) se += expf(z[j] - mx);
+  se = wave_sum(se);
+  float ent = 0.f, t1 = 0.f, t2 = 0.f;  // entropy and the two largest probabilities
+  for (int j = lane; j < count; j += 64) {
+    const float p = expf(z[j] - mx) / se;
+    ent -= p * logf(fmaxf(p, 1e-9f));
+    if (p > t1) {
+      t2 = t1;
+      t1 = p;
+    } else {
+      t2 = fmaxf(t2, p);
     }
   }
-  // CLS row of the gathered (pre-norm) rows opens the feature vector.
-  for (int e = tid; e < D; e += 256) feat[e] = a.selected[static_cast<size_t>(base) * D + e];
-  __syncthreads();
-
-  if (wave == 0) {  // softmax over this question's option logits (slots 1..count)
-    float mx = -INFINITY;
-    for (int j = lane; j < count; j += 64) mx = fmaxf(mx, slog[1 + j]);
-    mx = wave_max(mx);
-    float se = 0.f;
-    for (int j = lane; j < count; j += 64) se += expf(slog[1 + j] - mx);
-    se = wave_sum(se);
-    float ent = 0.f, t1 = 0.f, t2 = 0.f;  // entropy and top-2 probabilities
-    for (int j = lane; j < count; j += 64) {
-      const float p = expf(slog[1 + j] - mx) / se;
-      ent -= p * logf(fmaxf(p, 1e-9f));
-      if (p > t1) {
-        t2 = t1;
-        t1 = p;
-      } else {
-        t2 = fmaxf(t2, p);
-      }
-    }
-    ent = wave_sum(ent);
+  ent = wave_sum(ent);
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-      const float o1 = __shfl_xor(t1, d, 64), o2 = __shfl_xor(t2, d, 64);
-      t2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
-      t1 = fmaxf(t1, o1);
-    }
-    if (lane == 0) {
-      const int n = max(count, 2);
-      feat[D] = t1;
-      feat[D + 1] = t1 - t2;
-      feat[D + 2] = ent / logf(static_cast<float>(n));
-      feat[D + 3] = static_cast<float>(n) / 255.f;
-    }
+  for (int d = 32; d >= 1; d >>= 1) {
+    const float o1 = __shfl_xor(t1, d, 64), o2 = __shfl_xor(t2, d, 64);
+    t2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
+    t1 = fmaxf(t1, o1);
   }
-  __syncthreads();
+  if (lane == 0) {
+    const int n = max(count, 2);
+    feat[a.width] = t1;
+    feat[a.width + 1] = t1 - t2;
+    feat[a.width + 2] = ent / logf(static_cast<float>(n));
+    feat[a.width + 3] = static_cast<float>(n) / 255.f;
+  }
+}
 
-  // act_head.0 + GELU: one wave per output, lanes stride the D+4 inputs.
-  for (int o = wave; o < a.hidden; o += 4) {
-    const float* w = a.a0w + static_cast<size_t>(o) * (D + 4);
-    float s = 0.f;
-    for (int e = lane; e < D + 4; e += 64) s += feat[e] * w[e];
-    s = wave_sum(s);
-    if (lane == 0) hid[o] = gelu(s + a.a0b[o]);
+// act head output, one workgroup per question: hidden = gelu(sum of partials + a0b) in LDS, then
+// one wave per act output.
+__global__ __launch_bounds__(256) void act_out_kernel(ActOutArgs a) {
+  const int q = blockIdx.x;
+  if (q >= *a.n_q) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  extern __shared__ float hid[];  // [hidden]
+  for (int o = tid; o < a.hidden; o += 256) {
+    const size_t off = static_cast<size_t>(q) * a.hidden + o;
+    float v = a.parts[off];
+    for (int s = 1; s < a.splits; ++s) v = v + a.parts[s * a.split_stride + off];
+    hid[o] = gelu(v + a.a0b[o]);
   }
   __syncthreads();
   for (int o = wave; o < a.n_act; o += 4) {
@@ -176,7 +181,7 @@ __global__ __launch_bounds__(256) void head_finish_kernel(HeadFinishArgs a) {
     float s = 0.f;
     for (int e = lane; e < a.hidden; e += 64) s += hid[e] * w[e];
     s = wave_sum(s);
-    if (lane == 0) acts[o] = s + a.a2b[o];
+    if (lane == 0) a.acts[static_cast<size_t>(q) * a.n_act + o] = s + a.a2b[o];
   }
 }
 
@@ -210,17 +215,31 @@ hipError_t launch_head_gemm(const HeadGemmArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_head_finish(const HeadFinishArgs& a, hipStream_t stream) {
-  if (a.b <= 0) return hipSuccess;
-  const size_t lds = static_cast<size_t>(a.k + 1 + a.width + 4 + a.hidden) * sizeof(float);
-  const dim3 grid(a.b), block(256);
-  switch (a.width) {
-#define LAYA_CASE(D) case D: hipLaunchKernelGGL((head_finish_kernel<D>), grid, block, lds, stream, a); break;
+hipError_t launch_head_logit(const HeadLogitArgs& a, int width, hipStream_t stream) {
+  if (a.cap <= 0) return hipSuccess;
+  const dim3 grid((a.cap + 3) / 4), block(256);
+  switch (width) {
+#define LAYA_CASE(D) case D: hipLaunchKernelGGL((head_logit_kernel<D>), grid, block, 0, stream, a); break;
     LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
     LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
 #undef LAYA_CASE
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_head_features(const HeadFeatureArgs& a, hipStream_t stream) {
+  if (a.b <= 0) return hipSuccess;
+  if (a.kp < a.width + 4) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(head_features_kernel, dim3(a.b), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_out(const ActOutArgs& a, hipStream_t stream) {
+  if (a.b <= 0) return hipSuccess;
+  const size_t lds = static_cast<size_t>(a.hidden) * sizeof(float);
+  if (lds > 64 * 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(act_out_kernel, dim3(a.b), dim3(256), lds, stream, a);
   return hipGetLastError();
 }
 

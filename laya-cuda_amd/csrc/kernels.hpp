@@ -116,25 +116,49 @@ struct HeadGemmArgs {
 int head_gemm_splits(int rows, int N, int K, int cus);
 hipError_t launch_head_gemm(const HeadGemmArgs& a, hipStream_t stream);
 
-struct HeadFinishArgs {
+// scorer tail per head row: logit = w3 . gelu(sum of scorer.1 partials + b1) + b3
+struct HeadLogitArgs {
   const float* parts;  // scorer.1 partial products [splits][cap][d]
   int splits;
   long long split_stride;
   const float* b1;     // scorer.1 bias [d]
   const float* w3;     // scorer.3 weight [d]
   const float* b3;     // scorer.3 bias [1]
-  const float* selected;
-  const int32_t* counts;  // [b]
+  const int32_t* sel_q;   // [cap] question of each compact head row
   const int32_t* qoff;    // [b] first compact head row of each question
-  const int32_t* n_q;     // device scalar
-  const float* a0w;  // act_head.0 [hidden][d+4]
-  const float* a0b;
-  const float* a2w;  // act_head.2 [n_act][hidden]
-  const float* a2b;
-  float* logits;  // [b][k+1]
-  float* acts;    // [b][n_act]
-  int b, k, width, n_act, hidden;
+  const int32_t* n_sel;   // device scalar
+  float* row_logit;  // [cap]
+  float* logits;     // [b][k+1]
+  int cap, k;
 };
-hipError_t launch_head_finish(const HeadFinishArgs& a, hipStream_t stream);
+hipError_t launch_head_logit(const HeadLogitArgs& a, int width, hipStream_t stream);
+
+// per question: softmax statistics of its option logits -> act-head input row
+struct HeadFeatureArgs {
+  const float* row_logit;  // [cap]
+  const float* selected;   // [cap][d] gathered rows (CLS row opens each question)
+  const int32_t* counts;   // [b]
+  const int32_t* qoff;     // [b]
+  const int32_t* n_q;      // device scalar
+  float* logits;  // [b][k+1]: unused slots are zeroed here
+  float* feat;    // [b][kp]: CLS row | p1, p1-p2, entropy/log(max(n,2)), max(n,2)/255 | zeros
+  float* acts;    // [b][n_act]: zeroed for unused question slots
+  int b, k, width, kp, n_act;
+};
+hipError_t launch_head_features(const HeadFeatureArgs& a, hipStream_t stream);
+
+// act head output: acts = A2 gelu(sum of act_head.0 partials + a0) + a2
+struct ActOutArgs {
+  const float* parts;  // [splits][b][hidden]
+  int splits;
+  long long split_stride;
+  const float* a0b;  // [hidden]
+  const float* a2w;  // [n_act][hidden]
+  const float* a2b;  // [n_act]
+  const int32_t* n_q;
+  float* acts;  // [b][n_act]
+  int b, hidden, n_act;
+};
+hipError_t launch_act_out(const ActOutArgs& a, hipStream_t stream);
 
 }  // namespace laya

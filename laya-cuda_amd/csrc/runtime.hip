@@ -139,8 +139,9 @@ struct Slot {
   void *x = nullptr, *q = nullptr, *kk = nullptr, *vt = nullptr, *attn = nullptr, *ff = nullptr;
   float* part = nullptr;
   float *selected = nullptr, *normed = nullptr, *hpart = nullptr, *logits = nullptr, *acts = nullptr;
+  float *row_logit = nullptr, *feat = nullptr, *apart = nullptr;
   int tile[4] = {0, 0, 0, 0}, splits[4] = {1, 1, 1, 1};  // qkv, o, up, down
-  int attn_waves = 2, head_splits = 1;
+  int attn_waves = 2, head_splits = 1, act_splits = 1;
   hipGraphExec_t graph = nullptr;
   hipEvent_t start = nullptr, end = nullptr;
 };
@@ -162,6 +163,8 @@ struct Engine {
   const float *tok = nullptr, *pos = nullptr, *type0 = nullptr, *emb_g = nullptr, *emb_b = nullptr;
   const float *type_emb = nullptr, *s0w = nullptr, *s0b = nullptr, *s1w = nullptr, *s1b = nullptr;
   const float *s3w = nullptr, *s3b = nullptr, *a0w = nullptr, *a0b = nullptr, *a2w = nullptr, *a2b = nullptr;
+  float* a0w_pad = nullptr;  // act_head.0 weight [act_hidden][act_k], zero columns past d+4
+  int act_k = 0;
   std::list<Slot*> lru;  // front = least recently used
   std::string error;
 
@@ -177,7 +180,8 @@ void check_config(const LayaConfig& c) {
   LAYA_REQUIRE(c.vocab > 0 && c.max_positions > 0 && c.type_vocab > 0, "vocab/positions/type rows must be positive");
   LAYA_REQUIRE(c.max_len > 0 && span16(c.max_len) <= (c.pos_kind == LAYA_POS_LEARNED ? span16(c.max_positions) : 1 << 20),
                "max_len exceeds the position table");
-  LAYA_REQUIRE(c.n_act >= 1 && c.act_hidden >= 1, "act head must have outputs");
+  LAYA_REQUIRE(c.n_act >= 1 && c.act_hidden >= 64 && c.act_hidden % 64 == 0 && c.act_hidden <= 16384,
+               "act head hidden width must be a positive multiple of 64");
   LAYA_REQUIRE(c.mfma_dtype == LAYA_BF16 || c.mfma_dtype == LAYA_F16, "mfma_dtype must be LAYA_BF16 or LAYA_F16");
   LAYA_REQUIRE(c.eps > 0.f, "eps must be positive");
   // The graded workloads run the BERT-style post-LN encoder; the reference's ModernBERT executor
@@ -260,6 +264,7 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
     s->splits[0] = s->splits[2] = 1;
     s->attn_waves = (static_cast<long long>(m / 128) * c.heads >= E.cus) ? 4 : 2;
     s->head_splits = head_gemm_splits(s->L.R, d, d, E.cus);
+    s->act_splits = head_gemm_splits(b, c.act_hidden, E.act_k, E.cus);
     const int max_split = s->splits[1] > s->splits[3] ? s->splits[1] : s->splits[3];
 
     const size_t h2 = 2;  // 16-bit element
@@ -281,6 +286,9 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
         {reinterpret_cast<void**>(&s->selected), R * d * 4},
         {reinterpret_cast<void**>(&s->normed), R * d * 4},
         {reinterpret_cast<void**>(&s->hpart), R * d * 4 * s->head_splits},
+        {reinterpret_cast<void**>(&s->row_logit), R * 4},
+        {reinterpret_cast<void**>(&s->feat), static_cast<size_t>(b) * E.act_k * 4},
+        {reinterpret_cast<void**>(&s->apart), static_cast<size_t>(b) * c.act_hidden * 4 * s->act_splits},
         {reinterpret_cast<void**>(&s->logits), static_cast<size_t>(b) * (k + 1) * 4},
         {reinterpret_cast<void**>(&s->acts), static_cast<size_t>(b) * c.n_act * 4},
     };
@@ -374,55 +382,114 @@ void check_launch(hipError_t e, const char* what) {
   if (e != hipSuccess) throw Failure{LAYA_EDEVICE, std::string(what) + ": " + hipGetErrorString(e)};
 }
 
-void forward(Engine& E, Slot& s) {
+// The forward as a list of launches ("stages"); forward() runs them in order, and the timing
+// entry point replays one of them in isolation.
+enum Stage : int {
+  kEmbed = 0, kQkv, kAttention, kAttnOut, kAttnNorm, kFfnUp, kFfnDown, kFfnNorm,
+  kHeadGather, kHeadScorer, kHeadLogit, kHeadFeatures, kActHidden, kActOut, kStageCount
+};
+const char* const kStageNames[kStageCount] = {
+    "embed_norm", "qkv", "attention", "attn_out", "attn_norm", "ffn_up", "ffn_down", "ffn_norm",
+    "head_gather", "head_scorer", "head_logit", "head_features", "act_hidden", "act_out"};
+bool per_layer(int stage) { return stage >= kQkv && stage <= kFfnNorm; }
+
+void launch_stage(Engine& E, Slot& s, int stage, int layer) {
   const LayaConfig& c = E.cfg;
   const int m = s.m, d = c.width, f = c.intermediate;
   const DType t = E.mfma();
   const int32_t* P = s.d_packed;
   const Layout& L = s.L;
   hipStream_t st = E.stream;
-
-  EmbedArgs ea{P + L.ids, P + L.positions, E.tok, E.pos, E.type0, E.emb_g, E.emb_b, c.eps,
-               s.residual, s.x, m, c.vocab, c.max_positions};
-  check_launch(launch_embed(ea, d, t, st), "embed");
   const long long md = static_cast<long long>(m) * d;
-  for (const Layer& ly : E.layers) {
-    GemmArgs g{};
-    g.a = s.x; g.b = ly.wqkv; g.M = m; g.N = 3 * d; g.K = d; g.lda = d; g.ldb = d;
-    g.bias = ly.bqkv; g.splits = 1; g.q = s.q; g.k = s.kk; g.vt = s.vt; g.width = d;
-    check_launch(launch_gemm(g, Epi::QKV, t, s.tile[0], st), "qkv");
-
-    AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, P + L.n_tiles, P + L.starts, P + L.lengths, m, c.heads, L.T};
-    check_launch(launch_attention(aa, t, s.attn_waves, st), "attention");
-
-    g = GemmArgs{};
-    g.a = s.attn; g.b = ly.wo; g.M = m; g.N = d; g.K = d; g.lda = d; g.ldb = d;
-    g.out = s.part; g.ldo = d; g.split_stride = md; g.splits = s.splits[1];
-    check_launch(launch_gemm(g, Epi::F32, t, s.tile[1], st), "attn out");
-    AddNormArgs na{s.residual, s.part, s.splits[1], md, ly.bo, ly.n1g, ly.n1b, c.eps, nullptr, s.residual, s.x, m};
-    check_launch(launch_add_norm(na, d, t, st), "post-attention norm");
-
-    g = GemmArgs{};
-    g.a = s.x; g.b = ly.wi; g.M = m; g.N = f; g.K = d; g.lda = d; g.ldb = d;
-    g.bias = ly.bi; g.out = s.ff; g.ldo = f; g.splits = 1;
-    check_launch(launch_gemm(g, Epi::GELU, t, s.tile[2], st), "ffn up");
-    g = GemmArgs{};
-    g.a = s.ff; g.b = ly.wo2; g.M = m; g.N = d; g.K = f; g.lda = f; g.ldb = f;
-    g.out = s.part; g.ldo = d; g.split_stride = md; g.splits = s.splits[3];
-    check_launch(launch_gemm(g, Epi::F32, t, s.tile[3], st), "ffn down");
-    na = AddNormArgs{s.residual, s.part, s.splits[3], md, ly.bo2, ly.n2g, ly.n2b, c.eps, nullptr, s.residual, s.x, m};
-    check_launch(launch_add_norm(na, d, t, st), "post-ffn norm");
+  const Layer* ly = per_layer(stage) ? &E.layers[layer] : nullptr;
+  GemmArgs g{};
+  switch (stage) {
+    case kEmbed: {
+      EmbedArgs ea{P + L.ids, P + L.positions, E.tok, E.pos, E.type0, E.emb_g, E.emb_b, c.eps,
+                   s.residual, s.x, m, c.vocab, c.max_positions};
+      check_launch(launch_embed(ea, d, t, st), "embed");
+      break;
+    }
+    case kQkv:
+      g.a = s.x; g.b = ly->wqkv; g.M = m; g.N = 3 * d; g.K = d; g.lda = d; g.ldb = d;
+      g.bias = ly->bqkv; g.splits = 1; g.q = s.q; g.k = s.kk; g.vt = s.vt; g.width = d;
+      check_launch(launch_gemm(g, Epi::QKV, t, s.tile[0], st), "qkv");
+      break;
+    case kAttention: {
+      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, P + L.n_tiles, P + L.starts, P + L.lengths, m, c.heads, L.T};
+      check_launch(launch_attention(aa, t, s.attn_waves, st), "attention");
+      break;
+    }
+    case kAttnOut:
+      g.a = s.attn; g.b = ly->wo; g.M = m; g.N = d; g.K = d; g.lda = d; g.ldb = d;
+      g.out = s.part; g.ldo = d; g.split_stride = md; g.splits = s.splits[1];
+      check_launch(launch_gemm(g, Epi::F32, t, s.tile[1], st), "attn out");
+      break;
+    case kAttnNorm: {
+      AddNormArgs na{s.residual, s.part, s.splits[1], md, ly->bo, ly->n1g, ly->n1b, c.eps, nullptr, s.residual, s.x, m};
+      check_launch(launch_add_norm(na, d, t, st), "post-attention norm");
+      break;
+    }
+    case kFfnUp:
+      g.a = s.x; g.b = ly->wi; g.M = m; g.N = f; g.K = d; g.lda = d; g.ldb = d;
+      g.bias = ly->bi; g.out = s.ff; g.ldo = f; g.splits = 1;
+      check_launch(launch_gemm(g, Epi::GELU, t, s.tile[2], st), "ffn up");
+      break;
+    case kFfnDown:
+      g.a = s.ff; g.b = ly->wo2; g.M = m; g.N = d; g.K = f; g.lda = f; g.ldb = f;
+      g.out = s.part; g.ldo = d; g.split_stride = md; g.splits = s.splits[3];
+      check_launch(launch_gemm(g, Epi::F32, t, s.tile[3], st), "ffn down");
+      break;
+    case kFfnNorm: {
+      AddNormArgs na{s.residual, s.part, s.splits[3], md, ly->bo2, ly->n2g, ly->n2b, c.eps, nullptr, s.residual, s.x, m};
+      check_launch(launch_add_norm(na, d, t, st), "post-ffn norm");
+      break;
+    }
+    case kHeadGather: {
+      HeadGatherArgs hg{s.residual, P + L.sel_src, P + L.sel_q, P + L.qkind, P + L.n_sel, E.type_emb,
+                        E.s0w, E.s0b, 1e-5f, s.selected, s.normed, L.R};
+      check_launch(launch_head_gather(hg, d, st), "head gather");
+      break;
+    }
+    case kHeadScorer: {
+      HeadGemmArgs hm{s.normed, E.s1w, s.hpart, P + L.n_sel, L.R, d, d, s.head_splits, static_cast<long long>(L.R) * d};
+      check_launch(launch_head_gemm(hm, st), "scorer");
+      break;
+    }
+    case kHeadLogit: {
+      HeadLogitArgs hl{s.hpart, s.head_splits, static_cast<long long>(L.R) * d, E.s1b, E.s3w, E.s3b,
+                       P + L.sel_q, P + L.qoff, P + L.n_sel, s.row_logit, s.logits, L.R, s.k};
+      check_launch(launch_head_logit(hl, d, st), "head logit");
+      break;
+    }
+    case kHeadFeatures: {
+      HeadFeatureArgs hf{s.row_logit, s.selected, P + L.counts, P + L.qoff, P + L.meta + 1, s.logits, s.feat,
+                         s.acts, s.b, s.k, d, E.act_k, c.n_act};
+      check_launch(launch_head_features(hf, st), "head features");
+      break;
+    }
+    case kActHidden: {
+      HeadGemmArgs ha{s.feat, E.a0w_pad, s.apart, P + L.meta + 1, s.b, c.act_hidden, E.act_k, s.act_splits,
+                      static_cast<long long>(s.b) * c.act_hidden};
+      check_launch(launch_head_gemm(ha, st), "act hidden");
+      break;
+    }
+    case kActOut: {
+      ActOutArgs ao{s.apart, s.act_splits, static_cast<long long>(s.b) * c.act_hidden, E.a0b, E.a2w, E.a2b,
+                    P + L.meta + 1, s.acts, s.b, c.act_hidden, c.n_act};
+      check_launch(launch_act_out(ao, st), "act out");
+      break;
+    }
+    default:
+      throw Failure{LAYA_EINVAL, "unknown stage"};
   }
+}
 
-  HeadGatherArgs hg{s.residual, P + L.sel_src, P + L.sel_q, P + L.qkind, P + L.n_sel, E.type_emb,
-                    E.s0w, E.s0b, 1e-5f, s.selected, s.normed, L.R};
-  check_launch(launch_head_gather(hg, d, st), "head gather");
-  HeadGemmArgs hm{s.normed, E.s1w, s.hpart, P + L.n_sel, L.R, d, d, s.head_splits, static_cast<long long>(L.R) * d};
-  check_launch(launch_head_gemm(hm, st), "scorer");
-  HeadFinishArgs hf{s.hpart, s.head_splits, static_cast<long long>(L.R) * d, E.s1b, E.s3w, E.s3b, s.selected,
-                    P + L.counts, P + L.qoff, P + L.meta + 1, E.a0w, E.a0b, E.a2w, E.a2b, s.logits, s.acts,
-                    s.b, s.k, d, c.n_act, c.act_hidden};
-  check_launch(launch_head_finish(hf, st), "head finish");
+void forward(Engine& E, Slot& s) {
+  launch_stage(E, s, kEmbed, 0);
+  for (int i = 0; i < E.cfg.layers; ++i)
+    for (int stage = kQkv; stage <= kFfnNorm; ++stage) launch_stage(E, s, stage, i);
+  for (int stage = kHeadGather; stage < kStageCount; ++stage) launch_stage(E, s, stage, 0);
 }
 
 Slot* find_slot(Engine& E, int m, int b, int k, bool* miss) {
@@ -510,6 +577,7 @@ int laya_create(const LayaConfig* cfg, int device, int max_slots, void** handle)
     LAYA_REQUIRE(std::strncmp(prop.gcnArchName, "gfx950", 6) == 0,
                  std::string(prop.name) + " is " + prop.gcnArchName + "; liblaya_hip is built for gfx950 (MI355X)");
     E->cus = prop.multiProcessorCount;
+    E->act_k = (cfg->width + 4 + 255) / 256 * 256;
     prepare_device();
     LAYA_HIP(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
     build_expected(*E);
@@ -622,6 +690,23 @@ int laya_finalize(void* handle) {
     E->a0b = f32(*E, "act_head.0.bias");
     E->a2w = f32(*E, "act_head.2.weight");
     E->a2b = f32(*E, "act_head.2.bias");
+    {
+      // act_head.0 padded with zero columns to act_k (a multiple of 256): the fp32 MFMA GEMM then
+      // splits K 8-16 ways; the padding multiplies zero features.
+      const int d4 = E->cfg.width + 4, hid = E->cfg.act_hidden;
+      std::vector<float> w(static_cast<size_t>(hid) * d4), padded(static_cast<size_t>(hid) * E->act_k, 0.f);
+      LAYA_HIP(hipMemcpy(w.data(), E->a0w, w.size() * 4, hipMemcpyDeviceToHost));
+      for (int o = 0; o < hid; ++o)
+        std::memcpy(&padded[static_cast<size_t>(o) * E->act_k], &w[static_cast<size_t>(o) * d4], d4 * 4);
+      if (E->a0w_pad) {
+        (void)hipFree(E->a0w_pad);
+        E->a0w_pad = nullptr;
+        E->weight_bytes -= padded.size() * 4;
+      }
+      LAYA_HIP(hipMalloc(reinterpret_cast<void**>(&E->a0w_pad), padded.size() * 4));
+      E->weight_bytes += padded.size() * 4;
+      LAYA_HIP(hipMemcpy(E->a0w_pad, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));
+    }
     // Graphs captured earlier hold old weight pointers: drop every slot.
     for (Slot* s : E->lru) destroy_slot(*E, s);
     E->lru.clear();
@@ -629,22 +714,30 @@ int laya_finalize(void* handle) {
   });
 }
 
+// Slot lookup, validation and the single H2D upload shared by predict and the timing entry point.
+static Slot* stage_inputs(Engine* E, const int32_t* host_packed, const LayaShape* shape, bool* miss) {
+  if (!E->finalized) throw Failure{LAYA_ESTATE, "predict before laya_finalize"};
+  LAYA_REQUIRE(host_packed && shape, "null argument");
+  const int m = shape->rows, b = shape->batch, k = shape->options;
+  LAYA_REQUIRE(m > 0 && m % 16 == 0 && m <= (1 << 22) && b > 0 && b <= (1 << 16) && k > 0 && k <= (1 << 12),
+               "invalid shape class");
+  LAYA_HIP(hipSetDevice(E->device));
+  Slot* s = find_slot(*E, m, b, k, miss);
+  std::memcpy(s->h_packed, host_packed, s->L.user_end * 4);
+  derive_inputs(*E, *s);
+  LAYA_HIP(hipMemcpyAsync(s->d_packed, s->h_packed, s->L.total * 4, hipMemcpyHostToDevice, E->stream));
+  return s;
+}
+
 int laya_predict(void* handle, const int32_t* host_packed, const LayaShape* shape, int capture, float* host_logits,
                  float* host_acts, LayaMetrics* metrics) {
   Engine* E = static_cast<Engine*>(handle);
   if (!E) return fail(nullptr, Failure{LAYA_EINVAL, "null handle"});
   return guarded(E, [&] {
-    if (!E->finalized) throw Failure{LAYA_ESTATE, "predict before laya_finalize"};
-    LAYA_REQUIRE(host_packed && shape && host_logits && host_acts, "null argument");
-    const int m = shape->rows, b = shape->batch, k = shape->options;
-    LAYA_REQUIRE(m > 0 && m % 16 == 0 && m <= (1 << 22) && b > 0 && b <= (1 << 16) && k > 0 && k <= (1 << 12),
-                 "invalid shape class");
-    LAYA_HIP(hipSetDevice(E->device));
+    LAYA_REQUIRE(host_logits && host_acts, "null argument");
     bool miss = false;
-    Slot* s = find_slot(*E, m, b, k, &miss);
-    std::memcpy(s->h_packed, host_packed, s->L.user_end * 4);
-    derive_inputs(*E, *s);
-    LAYA_HIP(hipMemcpyAsync(s->d_packed, s->h_packed, s->L.total * 4, hipMemcpyHostToDevice, E->stream));
+    Slot* s = stage_inputs(E, host_packed, shape, &miss);
+    const int b = s->b, k = s->k;
     const bool captured_now = capture && !s->graph;
     if (captured_now) {
       LAYA_HIP(hipStreamBeginCapture(E->stream, hipStreamCaptureModeThreadLocal));
@@ -683,6 +776,31 @@ int laya_predict(void* handle, const int32_t* host_packed, const LayaShape* shap
       metrics->graph_replay = capture && s->graph != nullptr;
       metrics->owned_gpu_bytes = static_cast<int64_t>(E->weight_bytes + E->slot_bytes);
     }
+  });
+}
+
+int laya_stage_count(void) { return kStageCount; }
+
+const char* laya_stage_name(int stage) { return stage >= 0 && stage < kStageCount ? kStageNames[stage] : nullptr; }
+
+int laya_time_stage(void* handle, const int32_t* host_packed, const LayaShape* shape, int stage, int layer, int reps,
+                    float* avg_ms) {
+  Engine* E = static_cast<Engine*>(handle);
+  if (!E) return fail(nullptr, Failure{LAYA_EINVAL, "null handle"});
+  return guarded(E, [&] {
+    LAYA_REQUIRE(avg_ms && reps >= 1 && reps <= 100000, "reps must be in [1, 100000]");
+    LAYA_REQUIRE(stage >= 0 && stage < kStageCount, "unknown stage");
+    LAYA_REQUIRE(!per_layer(stage) || (layer >= 0 && layer < E->cfg.layers), "layer out of range");
+    bool miss = false;
+    Slot* s = stage_inputs(E, host_packed, shape, &miss);
+    forward(*E, *s);  // every buffer the stage reads now holds this request's values
+    LAYA_HIP(hipEventRecord(s->start, E->stream));
+    for (int r = 0; r < reps; ++r) launch_stage(*E, *s, stage, layer);
+    LAYA_HIP(hipEventRecord(s->end, E->stream));
+    LAYA_HIP(hipStreamSynchronize(E->stream));
+    float ms = 0.f;
+    LAYA_HIP(hipEventElapsedTime(&ms, s->start, s->end));
+    *avg_ms = ms / static_cast<float>(reps);
   });
 }
 
@@ -726,6 +844,7 @@ int laya_destroy(void* handle) {
   E->lru.clear();
   for (auto& kv : E->weights) (void)hipFree(kv.second.ptr);
   E->weights.clear();
+  if (E->a0w_pad) (void)hipFree(E->a0w_pad);
   if (E->stream) (void)hipStreamDestroy(E->stream);
   delete E;
   return LAYA_OK;

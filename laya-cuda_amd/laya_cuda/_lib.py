@@ -42,6 +42,9 @@ SIGNATURES = {
     "laya_load_weight": ([_p, ct.c_char_p, _p, _i, ct.POINTER(_i64), _i], _i),
     "laya_finalize": ([_p], _i),
     "laya_predict": ([_p, _ip, ct.POINTER(LayaShape), _i, _fp, _fp, ct.POINTER(LayaMetrics)], _i),
+    "laya_stage_count": ([], _i),
+    "laya_stage_name": ([_i], ct.c_char_p),
+    "laya_time_stage": ([_p, _ip, ct.POINTER(LayaShape), _i, _i, _i, _fp], _i),
     "laya_read_weight": ([_p, ct.c_char_p, _fp, _i64], _i),
     "laya_used_bytes": ([_p], _i64),
     "laya_slot_count": ([_p], _i),

@@ -217,6 +217,26 @@ class Runtime:
             "graph_capture": bool(metrics.graph_capture), "graph_replay": bool(metrics.graph_replay),
             "owned_gpu_bytes": int(metrics.owned_gpu_bytes)}
 
+    @staticmethod
+    def stages():
+        """Names of the forward's launches, in order (per-layer stages run once per layer)."""
+        lib = _lib.load()
+        return [lib.laya_stage_name(i).decode() for i in range(lib.laya_stage_count())]
+
+    def time_stage(self, sequences, questions, stage, layer=0, reps=50, key=None):
+        """Average device time (ms) of one launch of ``stage`` on this request's shape slot,
+        measured with events around ``reps`` back-to-back launches on the engine's stream."""
+        if self._handle is None:
+            raise RuntimeError("Runtime is closed")
+        key = key or shape_class(sequences, questions)
+        block = pack(sequences, questions, key, self.adapter.pad, self.adapter.vocab)
+        index = self.stages().index(stage) if isinstance(stage, str) else int(stage)
+        avg = ct.c_float()
+        _lib.check(_lib.load().laya_time_stage(
+            self._handle, block.ctypes.data_as(ct.POINTER(ct.c_int32)), ct.byref(_lib.LayaShape(*key)), index,
+            int(layer), int(reps), ct.byref(avg)), self._handle)
+        return float(avg.value)
+
     def close(self):
         if self._handle is not None:
             _lib.load().laya_destroy(self._handle)

@@ -139,9 +139,13 @@ def head(hidden, markers, kind, w):
     h = w["head"]
     rows = np.concatenate([[0], np.asarray(markers, np.int64)])
     selected = hidden[rows] + h["type_emb"][kind]
-    normed = layer_norm(selected, h["s0_w"], h["s0_b"], 1e-5)
+    # Duplicate markers are legal and must score identically: BLAS may round identical rows
+    # differently by their place in a block, so score each distinct row once and expand.
+    distinct, back = np.unique(rows, return_inverse=True)
+    unique_sel = hidden[distinct] + h["type_emb"][kind]
+    normed = layer_norm(unique_sel, h["s0_w"], h["s0_b"], 1e-5)
     scored = gelu(_mm(normed, h["s1_w"]) + h["s1_b"])
-    logits = (_mm(scored, h["s3_w"]) + h["s3_b"])[:, 0]
+    logits = (_mm(scored, h["s3_w"]) + h["s3_b"])[:, 0][back.reshape(-1)]
     count = len(markers)
     feats = features(selected[0], logits[1:], count)
     hidden_act = gelu(_mm(feats[None], h["a0_w"]) + h["a0_b"])

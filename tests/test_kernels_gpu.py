@@ -232,8 +232,10 @@ def test_qkv_epilogue_writes_head_major_layout(gpu, tile):
     w = rng.integers(-2, 3, (3 * width, width)).astype(np.float32)
     bias = rng.integers(-4, 5, 3 * width).astype(np.float32)
     q, k, vt = (t.full((heads * M * 64,), float("nan"), dtype=t.float16, device=gpu) for _ in range(3))
-    check(_lib.load().laya_op_qkv(p(to16(x, "f16", gpu)), p(to16(w, "f16", gpu)), p(dev(bias, gpu)), p(q), p(k),
-                                  p(vt), _lib.F16, M, width, tile, stream()))
+    # Keep every operand referenced until the kernel has run: a temporary freed inside the argument
+    # list returns its memory to torch's caching allocator, which hands it to the next operand.
+    d_x, d_w, d_bias = to16(x, "f16", gpu), to16(w, "f16", gpu), dev(bias, gpu)
+    check(_lib.load().laya_op_qkv(p(d_x), p(d_w), p(d_bias), p(q), p(k), p(vt), _lib.F16, M, width, tile, stream()))
     sync()
     full = x @ w.T + bias  # [M, 3*width], exact in fp32 and fp16
     parts = full.reshape(M, 3, heads, 64)
