@@ -200,6 +200,7 @@ def run_extras(args):
         rt = Runtime(spec, 0, 2, weights=weights)
         try:
             r = time_workload(rt, sequences, questions, steps, min(args.warmup, 5), not args.eager)
+            rows = stage_profile(rt, spec, sequences, questions, 3 if name in ("ragged32", "b64x1024") else 20)
         finally:
             rt.close()
         progress(f"{name} timed: p50 {pct(r['gpu'], 50):.4f} ms")
@@ -210,6 +211,8 @@ def run_extras(args):
                  "first_ms": round(r["first_ms"], 3), "steps": steps,
                  "tflops": round(flops / (p50 * 1e-3) / 1e12, 2),
                  "mfma_frac": round(flops / (p50 * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)}
+        entry["stages_us_per_forward"] = {row["stage"]: round(row["forward_ms"] * 1e3, 2) for row in rows}
+        entry["stage_frac"] = {row["stage"]: round(roofline(row)["frac"], 4) for row in rows if row["bound"]}
         if len(sequences) > 1:
             entry["seqs_per_s"] = round(len(sequences) / (p50 * 1e-3), 1)
             entry["seqs_per_s_predict"] = round(len(sequences) / (pct(r["api"], 50) * 1e-3), 1)

@@ -114,7 +114,7 @@ int laya_predict(void* handle, const int32_t* host_packed, const LayaShape* shap
 /* Per-launch timing, the native counterpart of the reference's profiling hook that records events
  * around every Ops.call/linear (tools/profile_long.py:21-67).  The forward is a fixed list of
  * stages (embed_norm; per layer qkv, attention, attn_out, attn_norm, ffn_up, ffn_down, ffn_norm;
- * head_gather, head_scorer, head_finish).  laya_time_stage uploads the request like
+ * head_gather, head_scorer, head_logit, head_features, act_hidden, act_out).  laya_time_stage uploads the request like
  * laya_predict, runs one eager forward so every buffer holds this request's values, then launches
  * stage `stage` of layer `layer` `reps` times back to back between two events on the engine's
  * stream and stores the average per launch in *avg_ms.  Stages that normalise in place
@@ -143,7 +143,10 @@ int laya_abi_version(void);
  * (or -1 if max_tiles is too small).  Host-only. */
 int laya_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_seq, int m, int block,
                          int32_t* tiles, int max_tiles);
-int laya_attention_block(int waves);
+/* Query rows per tile of an attention kernel: mode 0 (K/V blocks staged once in LDS and shared by
+ * `waves` waves of 32 queries each; large batches) -> 32*waves; mode 1 (one tile of 32 queries whose
+ * keys are split across `waves` waves; batch-1 latency) -> 32.  -1 for an invalid pair. */
+int laya_attention_block(int mode, int waves);
 
 /* embed (kernels.cu:16-19) fused with the embeddings norm (runtime.py:93-95):
  * v = table[ids] (+ pos_table[positions]) (+ type_row); LayerNorm if gamma; writes out32 and/or
@@ -171,10 +174,11 @@ int laya_op_linear(const void* x, const void* w, const float* bias, void* out, i
 int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* k, void* vt,
                 int dtype16, int M, int width, int tile, void* stream);
 
-/* attention (kernels.cu:90-154, window -1) over a tile list from laya_attention_tiles. */
+/* attention (kernels.cu:90-154, window -1) over a tile list from laya_attention_tiles built with
+ * laya_attention_block(mode, waves) rows per tile. */
 int laya_op_attention(const void* q, const void* k, const void* vt, void* out,
                       const int32_t* tiles, const int32_t* n_tiles, const int32_t* starts,
-                      const int32_t* lengths, int m, int heads, int max_tiles, int waves,
+                      const int32_t* lengths, int m, int heads, int max_tiles, int mode, int waves,
                       int dtype16, void* stream);
 
 #ifdef __cplusplus

@@ -5,9 +5,9 @@
 // v_mfma_f32_32x32x16_{bf16,f16} operands want: each lane feeds 8 consecutive k of one row.
 //
 // Workgroup: 256 threads = 4 waves on a WM x WN grid; each wave owns (BM/WM) x (BN/WN) made of
-// 32x32 MFMA tiles.  K advances in 64-wide slabs staged through LDS, double-buffered: the next
-// slab's global loads are in flight (registers) while the current slab feeds the MFMAs, then
-// land in the other LDS buffer; one barrier per slab.  LDS rows are 128 B (64 x 16-bit) with the
+// 32x32 MFMA tiles.  K advances in 64-wide slabs staged through LDS, double-buffered; the global
+// loads of the next PF slabs are in flight in registers while the current slab feeds the MFMAs,
+// and each lands in the other LDS buffer one slab before its use; one barrier per slab.  LDS rows are 128 B (64 x 16-bit) with the
 // 16-byte chunk index XOR-swizzled by (row & 7), so the 32 lanes reading one k-chunk of 32
 // consecutive rows hit distinct banks.
 //
@@ -27,9 +27,10 @@ namespace {
 
 constexpr int BK = 64;
 
-template <typename T, int BM, int BN, int WM, int WN, Epi E>
+template <typename T, int BM, int BN, int WM, int WN, int PF, Epi E>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   static_assert(WM * WN == 4, "four waves per workgroup");
+  static_assert(PF >= 1, "at least one slab in flight");
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "32x32 MFMA tiles");
@@ -51,31 +52,30 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
   const int per = (nk + a.splits - 1) / a.splits;
   const int kb = z * per, ke = min(nk, kb + per);
 
-  i32x4 ra[ACH], rb[BCH];
-  auto gload = [&](int kt) {
+  auto gload = [&](int kt, i32x4 (&xa)[ACH], i32x4 (&xb)[BCH]) {
     const int k0 = kt * BK;
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
       const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
       const int g = min(m0 + row, a.M - 1);
-      ra[i] = *reinterpret_cast<const i32x4*>(A + static_cast<size_t>(g) * a.lda + k0 + ch * 8);
+      xa[i] = *reinterpret_cast<const i32x4*>(A + static_cast<size_t>(g) * a.lda + k0 + ch * 8);
     }
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
       const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
-      rb[i] = *reinterpret_cast<const i32x4*>(B + static_cast<size_t>(n0 + row) * a.ldb + k0 + ch * 8);
+      xb[i] = *reinterpret_cast<const i32x4*>(B + static_cast<size_t>(n0 + row) * a.ldb + k0 + ch * 8);
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, const i32x4 (&xa)[ACH], const i32x4 (&xb)[BCH]) {
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
       const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
-      *reinterpret_cast<i32x4*>(sA + buf * BM * BK + row * BK + ((ch ^ (row & 7)) << 3)) = ra[i];
+      *reinterpret_cast<i32x4*>(sA + buf * BM * BK + row * BK + ((ch ^ (row & 7)) << 3)) = xa[i];
     }
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
       const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
-      *reinterpret_cast<i32x4*>(sB + buf * BN * BK + row * BK + ((ch ^ (row & 7)) << 3)) = rb[i];
+      *reinterpret_cast<i32x4*>(sB + buf * BN * BK + row * BK + ((ch ^ (row & 7)) << 3)) = xb[i];
     }
   };
 
@@ -88,67 +88,98 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int lrow = lane & 31, kg = lane >> 5;
-  if (kb < ke) {
-    gload(kb);
-    lstore(0);
-    __syncthreads();
-    for (int kt = kb; kt < ke; ++kt) {
-      const int cur = (kt - kb) & 1;
-      if (kt + 1 < ke) gload(kt + 1);
-      const T* cA = sA + cur * BM * BK;
-      const T* cB = sB + cur * BN * BK;
+  auto compute = [&](int buf) {
+    const T* cA = sA + buf * BM * BK;
+    const T* cB = sB + buf * BN * BK;
 #pragma unroll
-      for (int kk = 0; kk < BK / 16; ++kk) {
-        const int ch = kk * 2 + kg;
-        T8 af[TM], bfr[TN];
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int ch = kk * 2 + kg;
+      T8 af[TM], bfr[TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          const int r = wm0 + i * 32 + lrow;
-          af[i] = *reinterpret_cast<const T8*>(cA + r * BK + ((ch ^ (r & 7)) << 3));
-        }
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int r = wn0 + j * 32 + lrow;
-          bfr[j] = *reinterpret_cast<const T8*>(cB + r * BK + ((ch ^ (r & 7)) << 3));
-        }
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(af[i], bfr[j], acc[i][j]);
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm0 + i * 32 + lrow;
+        af[i] = *reinterpret_cast<const T8*>(cA + r * BK + ((ch ^ (r & 7)) << 3));
       }
-      if (kt + 1 < ke) lstore(cur ^ 1);
-      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int r = wn0 + j * 32 + lrow;
+        bfr[j] = *reinterpret_cast<const T8*>(cB + r * BK + ((ch ^ (r & 7)) << 3));
+      }
+      // Weights as the MFMA A operand: the accumulator holds C^T, so each lane ends with four
+      // consecutive output columns of one row (vector stores in the epilogue).
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(bfr[j], af[i], acc[i][j]);
     }
+  };
+
+  // Pipeline: slab s >= 1 travels in register set (s-1) % PF, issued PF slabs ahead of its use, so
+  // PF slabs of global loads are in flight while the MFMAs consume the slab in LDS.  Two LDS
+  // buffers; one barrier per slab.  Every step issues its loads unconditionally (slab indices past
+  // the end are clamped to the last slab and never used), so the number of loads in flight is the
+  // same on every path and the compiler's wait counts keep the PF-1 younger sets in flight.
+  const int n = ke - kb;
+  if (n > 0) {
+    i32x4 ra[PF][ACH], rb[PF][BCH];
+    auto step = [&](int it, int u) {
+      compute(it & 1);
+      lstore((it + 1) & 1, ra[u], rb[u]);  // at it = n-1 this fills the idle buffer; never read
+      gload(kb + min(it + 1 + PF, n - 1), ra[u], rb[u]);
+      __syncthreads();
+    };
+    gload(kb, ra[0], rb[0]);
+    lstore(0, ra[0], rb[0]);
+#pragma unroll
+    for (int p = 0; p < PF; ++p) gload(kb + min(1 + p, n - 1), ra[p], rb[p]);
+    __syncthreads();
+    int it = 0;
+    for (; it + PF <= n; it += PF) {
+#pragma unroll
+      for (int u = 0; u < PF; ++u) step(it + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+      if (it + u < n) step(it + u, u);
   }
 
-  // Epilogue.  Element r of lane l in a 32x32 tile is row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+  // Epilogue.  Element r of lane l in a 32x32 tile of C^T is output column 8*(r/4) + 4*(l/32) +
+  // r%4 of output row l%32: a lane holds columns c..c+3 of one row for each r/4.
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
+    const int row = m0 + wm0 + i * 32 + lrow;
+    if (row >= a.M) continue;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int col = n0 + wn0 + j * 32 + lrow;
-      const float bias = (E != Epi::F32 || a.splits == 1) && a.bias ? a.bias[col] : 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * kg + (r & 3);
-        if (row >= a.M) continue;
-        const float v = acc[i][j][r] + bias;
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const int col = n0 + wn0 + j * 32 + 8 * r4 + 4 * kg;
+        float v[4] = {acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2], acc[i][j][4 * r4 + 3]};
+        if ((E != Epi::F32 || a.splits == 1) && a.bias) {
+          const float4 b = *reinterpret_cast<const float4*>(a.bias + col);
+          v[0] = v[0] + b.x; v[1] = v[1] + b.y; v[2] = v[2] + b.z; v[3] = v[3] + b.w;
+        }
         if constexpr (E == Epi::F32) {
-          static_cast<float*>(a.out)[z * a.split_stride + static_cast<long long>(row) * a.ldo + col] = v;
-        } else if constexpr (E == Epi::HALF) {
-          static_cast<T*>(a.out)[static_cast<long long>(row) * a.ldo + col] = to_half<T>(v);
-        } else if constexpr (E == Epi::GELU) {
-          static_cast<T*>(a.out)[static_cast<long long>(row) * a.ldo + col] = to_half<T>(gelu(v));
-        } else {
+          *reinterpret_cast<float4*>(static_cast<float*>(a.out) + z * a.split_stride +
+                                     static_cast<long long>(row) * a.ldo + col) = make_float4(v[0], v[1], v[2], v[3]);
+        } else if constexpr (E == Epi::QKV) {
           const int part = col / a.width, hn = col - part * a.width, head = hn >> 6, dim = hn & 63;
-          const T h = to_half<T>(v);
-          if (part == 0) {
-            static_cast<T*>(a.q)[(static_cast<size_t>(head) * a.M + row) * 64 + dim] = h;
-          } else if (part == 1) {
-            static_cast<T*>(a.k)[(static_cast<size_t>(head) * a.M + row) * 64 + dim] = h;
+          typename Vec4<T>::type h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = to_half<T>(v[e]);
+          if (part < 2) {
+            T* dst = static_cast<T*>(part == 0 ? a.q : a.k);
+            *reinterpret_cast<typename Vec4<T>::type*>(dst + (static_cast<size_t>(head) * a.M + row) * 64 + dim) = h;
           } else {
-            static_cast<T*>(a.vt)[(static_cast<size_t>(head) * 64 + dim) * a.M + row] = h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              static_cast<T*>(a.vt)[(static_cast<size_t>(head) * 64 + dim + e) * a.M + row] = h[e];
           }
+        } else {
+          typename Vec4<T>::type h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = to_half<T>(E == Epi::GELU ? gelu(v[e]) : v[e]);
+          *reinterpret_cast<typename Vec4<T>::type*>(static_cast<T*>(a.out) + static_cast<long long>(row) * a.ldo + col) = h;
         }
       }
     }
@@ -156,17 +187,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 }
 
 struct TileDef {
-  int bm, bn, wm, wn;
+  int bm, bn, wm, wn, pf;
 };
 // Tile menu; the planner picks per problem.  Ids are part of the op-level ABI (tests sweep them).
+// pf = K slabs of global loads in flight: deep for the small tiles of batch-1 problems, whose few
+// MFMAs per slab cannot cover HBM latency, shallow for the large tiles of batched problems.
 constexpr TileDef kTiles[] = {
-    {256, 256, 2, 2},  // 0: wave 128x128, large M (batched)
-    {256, 128, 2, 2},  // 1: wave 128x64
-    {128, 128, 2, 2},  // 2: wave 64x64
-    {128, 64, 2, 2},   // 3: wave 64x32
-    {64, 128, 2, 2},   // 4: wave 32x64
-    {64, 64, 2, 2},    // 5: wave 32x32, small M (batch-1 latency)
-    {32, 128, 1, 4},   // 6: wave 32x32, very small M
+    {256, 256, 2, 2, 1},  // 0: wave 128x128, large M (batched)
+    {256, 128, 2, 2, 1},  // 1: wave 128x64
+    {128, 128, 2, 2, 2},  // 2: wave 64x64
+    {128, 64, 2, 2, 3},   // 3: wave 64x32
+    {64, 128, 2, 2, 3},   // 4: wave 32x64
+    {64, 64, 2, 2, 4},    // 5: wave 32x32, small M (batch-1 latency)
+    {32, 128, 1, 4, 4},   // 6: wave 32x32, very small M
 };
 constexpr int kTileCount = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -178,15 +211,15 @@ hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
   const dim3 grid(a.N / d.bn, (a.M + d.bm - 1) / d.bm, a.splits), block(256);
   const size_t lds = lds_bytes(d.bm, d.bn);
   switch (tile) {
-#define LAYA_TILE(ID, BM_, BN_, WM_, WN_) \
-  case ID: hipLaunchKernelGGL((gemm_kernel<T, BM_, BN_, WM_, WN_, E>), grid, block, lds, stream, a); break;
-    LAYA_TILE(0, 256, 256, 2, 2)
-    LAYA_TILE(1, 256, 128, 2, 2)
-    LAYA_TILE(2, 128, 128, 2, 2)
-    LAYA_TILE(3, 128, 64, 2, 2)
-    LAYA_TILE(4, 64, 128, 2, 2)
-    LAYA_TILE(5, 64, 64, 2, 2)
-    LAYA_TILE(6, 32, 128, 1, 4)
+#define LAYA_TILE(ID, BM_, BN_, WM_, WN_, PF_) \
+  case ID: hipLaunchKernelGGL((gemm_kernel<T, BM_, BN_, WM_, WN_, PF_, E>), grid, block, lds, stream, a); break;
+    LAYA_TILE(0, 256, 256, 2, 2, 1)
+    LAYA_TILE(1, 256, 128, 2, 2, 1)
+    LAYA_TILE(2, 128, 128, 2, 2, 2)
+    LAYA_TILE(3, 128, 64, 2, 2, 3)
+    LAYA_TILE(4, 64, 128, 2, 2, 3)
+    LAYA_TILE(5, 64, 64, 2, 2, 4)
+    LAYA_TILE(6, 32, 128, 1, 4, 4)
 #undef LAYA_TILE
     default: return hipErrorInvalidValue;
   }
@@ -196,14 +229,14 @@ hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
 template <typename T, Epi E>
 hipError_t set_lds_attr() {
   hipError_t e = hipSuccess;
-#define LAYA_ATTR(BM_, BN_, WM_, WN_)                                                              \
-  if (e == hipSuccess)                                                                           \
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<T, BM_, BN_, WM_, WN_, E>), \
-                            hipFuncAttributeMaxDynamicSharedMemorySize,                            \
+#define LAYA_ATTR(BM_, BN_, WM_, WN_, PF_)                                                              \
+  if (e == hipSuccess)                                                                                \
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<T, BM_, BN_, WM_, WN_, PF_, E>), \
+                            hipFuncAttributeMaxDynamicSharedMemorySize,                                 \
                             static_cast<int>(lds_bytes(BM_, BN_)));
-  LAYA_ATTR(256, 256, 2, 2)
-  LAYA_ATTR(256, 128, 2, 2)
-  LAYA_ATTR(128, 128, 2, 2)
+  LAYA_ATTR(256, 256, 2, 2, 1)
+  LAYA_ATTR(256, 128, 2, 2, 1)
+  LAYA_ATTR(128, 128, 2, 2, 2)
 #undef LAYA_ATTR
   return e;
 }

@@ -85,8 +85,13 @@ struct AttnArgs {
   const int32_t* lengths;
   int m, heads, max_tiles;
 };
-int attention_block_rows(int waves);
-hipError_t launch_attention(const AttnArgs& a, DType t, int waves, hipStream_t stream);
+// Attention kernels: kAttnSharedKV - a workgroup of `waves` waves owns 32*waves queries and stages
+// each K/V block once in LDS for all of them (large batches); kAttnSplitKeys - a workgroup owns 32
+// queries and its `waves` waves split the keys, merging at the end (few query tiles: batch 1).
+enum AttnMode : int { kAttnSharedKV = 0, kAttnSplitKeys = 1 };
+int attention_block_rows(int mode, int waves);
+bool attention_mode_valid(int mode, int waves);
+hipError_t launch_attention(const AttnArgs& a, DType t, int mode, int waves, hipStream_t stream);
 
 // ---- decision head (no head transformer layers) ----
 struct HeadGatherArgs {

@@ -141,7 +141,7 @@ struct Slot {
   float *selected = nullptr, *normed = nullptr, *hpart = nullptr, *logits = nullptr, *acts = nullptr;
   float *row_logit = nullptr, *feat = nullptr, *apart = nullptr;
   int tile[4] = {0, 0, 0, 0}, splits[4] = {1, 1, 1, 1};  // qkv, o, up, down
-  int attn_waves = 2, head_splits = 1, act_splits = 1;
+  int attn_mode = 0, attn_waves = 2, head_splits = 1, act_splits = 1;
   hipGraphExec_t graph = nullptr;
   hipEvent_t start = nullptr, end = nullptr;
 };
@@ -262,7 +262,15 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
     gemm_plan(m, f, d, Epi::GELU, E.cus, &s->tile[2], &s->splits[2]);
     gemm_plan(m, d, f, Epi::F32, E.cus, &s->tile[3], &s->splits[3]);
     s->splits[0] = s->splits[2] = 1;
-    s->attn_waves = (static_cast<long long>(m / 128) * c.heads >= E.cus) ? 4 : 2;
+    // Few 128-query tiles (batch-1 requests): split each tile's keys across waves instead of
+    // sharing LDS-staged keys between query tiles, so the serial key loop is short.
+    if (static_cast<long long>(m / 128) * c.heads >= 2LL * E.cus) {
+      s->attn_mode = kAttnSharedKV;
+      s->attn_waves = 4;
+    } else {
+      s->attn_mode = kAttnSplitKeys;
+      s->attn_waves = 4;
+    }
     s->head_splits = head_gemm_splits(s->L.R, d, d, E.cus);
     s->act_splits = head_gemm_splits(b, c.act_hidden, E.act_k, E.cus);
     const int max_split = s->splits[1] > s->splits[3] ? s->splits[1] : s->splits[3];
@@ -328,7 +336,7 @@ void derive_inputs(const Engine& E, Slot& s) {
     LAYA_REQUIRE(P[L.positions + i] >= 0 && P[L.positions + i] < c.max_positions, "position out of range");
   }
   // Attention tiles: sequences in increasing start order, 16-aligned, non-overlapping.
-  const int block = attention_block_rows(s.attn_waves);
+  const int block = attention_block_rows(s.attn_mode, s.attn_waves);
   int32_t* tiles = P + L.tiles;
   int nt = 0, row = 0;
   auto zero_to = [&](int upto) {
@@ -417,7 +425,7 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       break;
     case kAttention: {
       AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, P + L.n_tiles, P + L.starts, P + L.lengths, m, c.heads, L.T};
-      check_launch(launch_attention(aa, t, s.attn_waves, st), "attention");
+      check_launch(launch_attention(aa, t, s.attn_mode, s.attn_waves, st), "attention");
       break;
     }
     case kAttnOut:
@@ -857,7 +865,9 @@ const char* laya_last_error(void* handle) {
 
 // ---------------- kernel-level entry points ----------------
 
-int laya_attention_block(int waves) { return attention_block_rows(waves); }
+int laya_attention_block(int mode, int waves) {
+  return attention_mode_valid(mode, waves) ? attention_block_rows(mode, waves) : -1;
+}
 
 int laya_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_seq, int m, int block, int32_t* tiles,
                          int max_tiles) {
@@ -947,11 +957,14 @@ int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* 
 
 int laya_op_attention(const void* q, const void* k, const void* vt, void* out, const int32_t* tiles,
                       const int32_t* n_tiles, const int32_t* starts, const int32_t* lengths, int m, int heads,
-                      int max_tiles, int waves, int dtype16, void* stream) {
+                      int max_tiles, int mode, int waves, int dtype16, void* stream) {
   return guarded(nullptr, [&] {
-    LAYA_REQUIRE(waves == 1 || waves == 2 || waves == 4, "waves must be 1, 2 or 4");
+    LAYA_REQUIRE(attention_mode_valid(mode, waves),
+                 "mode 0 (shared K/V) takes 1, 2 or 4 waves; mode 1 (split keys) takes 2, 4 or 8");
+    LAYA_REQUIRE(m % 16 == 0, "rows must be a multiple of 16");
     AttnArgs a{q, k, vt, out, tiles, n_tiles, starts, lengths, m, heads, max_tiles};
-    check_launch(launch_attention(a, half_type(dtype16), waves, static_cast<hipStream_t>(stream)), "attention");
+    check_launch(launch_attention(a, half_type(dtype16), mode, waves, static_cast<hipStream_t>(stream)),
+                 "attention");
   });
 }
 

@@ -51,12 +51,12 @@ SIGNATURES = {
     "laya_destroy": ([_p], _i),
     "laya_last_error": ([_p], ct.c_char_p),
     "laya_attention_tiles": ([_ip, _ip, _i, _i, _i, _ip, _i], _i),
-    "laya_attention_block": ([_i], _i),
+    "laya_attention_block": ([_i, _i], _i),
     "laya_op_embed": ([_p, _p, _p, _p, _p, _p, _p, _f, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "laya_op_norm": ([_p, _p, _i, _i64, _p, _p, _p, _f, _p, _p, _p, _i, _i, _i, _p], _i),
     "laya_op_linear": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p], _i),
     "laya_op_qkv": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p], _i),
-    "laya_op_attention": ([_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "laya_op_attention": ([_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p], _i),
 }
 
 _lib = None

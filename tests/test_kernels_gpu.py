@@ -250,10 +250,10 @@ def span(n):
     return -(-n // 16) * 16
 
 
-@pytest.mark.parametrize("waves", [1, 2, 4])
+@pytest.mark.parametrize("mode,waves", [(0, 1), (0, 2), (0, 4), (1, 2), (1, 4), (1, 8)])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("lengths", [[32], [7, 96], [128, 1], [250, 131], [256, 219, 145], [500], [1024, 333]])
-def test_packed_attention_matches_float64(gpu, lengths, dtype, waves):
+def test_packed_attention_matches_float64(gpu, lengths, dtype, mode, waves):
     """tests/test_attention.py:12-56 of the reference (window -1): ragged packed rows, tokens past
     the last row, NaN-poisoned output, padding queries exactly zero."""
     t = torch()
@@ -266,7 +266,7 @@ def test_packed_attention_matches_float64(gpu, lengths, dtype, waves):
     k = x[:, 1].transpose(1, 0, 2).copy()
     vt = x[:, 2].transpose(1, 2, 0).copy()             # [h][64][m]
     max_tiles = m // 16
-    block = lib.laya_attention_block(waves)
+    block = lib.laya_attention_block(mode, waves)
     tiles = np.zeros(3 * max_tiles, np.int32)
     lens = np.asarray(lengths, np.int32)
     n = lib.laya_attention_tiles(starts.ctypes.data_as(ct.POINTER(ct.c_int32)), lens.ctypes.data_as(ct.POINTER(ct.c_int32)),
@@ -277,7 +277,7 @@ def test_packed_attention_matches_float64(gpu, lengths, dtype, waves):
                                                                                        starts, lens)]
 
     def run():
-        check(lib.laya_op_attention(*[p(a) for a in args], m, h, max_tiles, waves, DTYPES[dtype][0], stream()))
+        check(lib.laya_op_attention(*[p(a) for a in args], m, h, max_tiles, mode, waves, DTYPES[dtype][0], stream()))
         sync()
         return from16(out)
 
