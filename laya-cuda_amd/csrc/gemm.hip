@@ -4,8 +4,9 @@
 // cublasGemmEx orientation at laya_cuda/ops.py:63-64), which is exactly what the gfx950
 // v_mfma_f32_32x32x16_{bf16,f16} operands want: each lane feeds 8 consecutive k of one row.
 //
-// Workgroup: 256 threads = 4 waves on a WM x WN grid; each wave owns (BM/WM) x (BN/WN) made of
-// 32x32 MFMA tiles.  K advances in 64-wide slabs staged through LDS, double-buffered; the global
+// Workgroup: 4 or 8 waves on a WM x WN grid; each wave owns (BM/WM) x (BN/WN) made of
+// 32x32 MFMA tiles (8 waves put two waves on each SIMD of the CU, so one issues MFMAs while the
+// other waits on LDS or a barrier).  K advances in 64-wide slabs staged through LDS, double-buffered; the global
 // loads of the next PF slabs are in flight in registers while the current slab feeds the MFMAs,
 // and each lands in the other LDS buffer one slab before its use; one barrier per slab.  LDS rows are 128 B (64 x 16-bit) with the
 // 16-byte chunk index XOR-swizzled by (row & 7), so the 32 lanes reading one k-chunk of 32
@@ -27,15 +28,44 @@ namespace {
 
 constexpr int BK = 64;
 
+// Workgroup tile coordinates.  Workgroups are dealt to the 8 XCDs round-robin by linear id, so
+// consecutive ids run on different L2s.  When the tile count allows, each XCD instead gets a
+// contiguous share of the tile space, walked in groups of 4 tile rows (columns), column (row)
+// index outer: the operand that is larger in HBM (A for many rows, B otherwise) is then fetched
+// into one XCD's L2 once and reused from there, and the group keeps the smaller operand's tile
+// resident while it is reused 4 times.
+__device__ __forceinline__ void tile_coords(int nx, int ny, bool rows_major, int* x, int* y) {
+  const int id = blockIdx.x + nx * blockIdx.y;
+  const int total = nx * ny;
+  if (total % 8) {
+    *x = blockIdx.x;
+    *y = blockIdx.y;
+    return;
+  }
+  const int t = (id % 8) * (total / 8) + id / 8;
+  constexpr int G = 4;
+  if (rows_major) {
+    const int group = t / (G * nx), first = group * G, size = min(G, ny - first), in = t - group * G * nx;
+    *y = first + in % size;
+    *x = in / size;
+  } else {
+    const int group = t / (G * ny), first = group * G, size = min(G, nx - first), in = t - group * G * ny;
+    *x = first + in % size;
+    *y = in / size;
+  }
+}
+
 template <typename T, int BM, int BN, int WM, int WN, int PF, Epi E>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
-  static_assert(WM * WN == 4, "four waves per workgroup");
+__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
+  constexpr int NT = 64 * WM * WN;
+  static_assert(WM * WN == 4 || WM * WN == 8, "four or eight waves per workgroup");
   static_assert(PF >= 1, "at least one slab in flight");
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "32x32 MFMA tiles");
-  constexpr int ACH = BM * 8 / 256;  // 16-byte chunks per thread per slab
-  constexpr int BCH = BN * 8 / 256;
+  constexpr int ACH = BM * 8 / NT;  // 16-byte chunks per thread per slab
+  constexpr int BCH = BN * 8 / NT;
+  static_assert(ACH >= 1 && BCH >= 1 && ACH * NT == BM * 8 && BCH * NT == BN * 8, "whole chunks per thread");
   typedef typename Vec8<T>::type T8;
 
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -44,7 +74,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM, z = blockIdx.z;
+  int tx, ty;
+  tile_coords(gridDim.x, gridDim.y, a.rows_major, &tx, &ty);
+  const int n0 = tx * BN, m0 = ty * BM, z = blockIdx.z;
 
   const T* A = static_cast<const T*>(a.a);
   const T* B = static_cast<const T*>(a.b);
@@ -56,25 +88,25 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
     const int k0 = kt * BK;
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
-      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
       const int g = min(m0 + row, a.M - 1);
       xa[i] = *reinterpret_cast<const i32x4*>(A + static_cast<size_t>(g) * a.lda + k0 + ch * 8);
     }
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
-      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
       xb[i] = *reinterpret_cast<const i32x4*>(B + static_cast<size_t>(n0 + row) * a.ldb + k0 + ch * 8);
     }
   };
   auto lstore = [&](int buf, const i32x4 (&xa)[ACH], const i32x4 (&xb)[BCH]) {
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
-      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
       *reinterpret_cast<i32x4*>(sA + buf * BM * BK + row * BK + ((ch ^ (row & 7)) << 3)) = xa[i];
     }
 #pragma unroll
     for (int i = 0; i < BCH; ++i) {
-      const int c = tid + 256 * i, row = c >> 3, ch = c & 7;
+      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
       *reinterpret_cast<i32x4*>(sB + buf * BN * BK + row * BK + ((ch ^ (row & 7)) << 3)) = xb[i];
     }
   };
@@ -178,7 +210,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
         } else {
           typename Vec4<T>::type h;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = to_half<T>(E == Epi::GELU ? gelu(v[e]) : v[e]);
+          for (int e = 0; e < 4; ++e) h[e] = to_half<T>(E == Epi::GELU ? gelu16(v[e]) : v[e]);
           *reinterpret_cast<typename Vec4<T>::type*>(static_cast<T*>(a.out) + static_cast<long long>(row) * a.ldo + col) = h;
         }
       }
@@ -188,6 +220,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs a) {
 
 struct TileDef {
   int bm, bn, wm, wn, pf;
+  int threads() const { return 64 * wm * wn; }
 };
 // Tile menu; the planner picks per problem.  Ids are part of the op-level ABI (tests sweep them).
 // pf = K slabs of global loads in flight: deep for the small tiles of batch-1 problems, whose few
@@ -200,6 +233,9 @@ constexpr TileDef kTiles[] = {
     {64, 128, 2, 2, 3},   // 4: wave 32x64
     {64, 64, 2, 2, 4},    // 5: wave 32x32, small M (batch-1 latency)
     {32, 128, 1, 4, 4},   // 6: wave 32x32, very small M
+    {256, 256, 2, 4, 1},  // 7: 8 waves of 128x64, large M
+    {256, 128, 4, 2, 1},  // 8: 8 waves of 64x64
+    {128, 256, 2, 4, 1},  // 9: 8 waves of 64x64
 };
 constexpr int kTileCount = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -208,7 +244,7 @@ constexpr size_t lds_bytes(int bm, int bn) { return static_cast<size_t>(2) * (bm
 template <typename T, Epi E>
 hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
   const TileDef& d = kTiles[tile];
-  const dim3 grid(a.N / d.bn, (a.M + d.bm - 1) / d.bm, a.splits), block(256);
+  const dim3 grid(a.N / d.bn, (a.M + d.bm - 1) / d.bm, a.splits), block(d.threads());
   const size_t lds = lds_bytes(d.bm, d.bn);
   switch (tile) {
 #define LAYA_TILE(ID, BM_, BN_, WM_, WN_, PF_) \
@@ -220,6 +256,9 @@ hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
     LAYA_TILE(4, 64, 128, 2, 2, 3)
     LAYA_TILE(5, 64, 64, 2, 2, 4)
     LAYA_TILE(6, 32, 128, 1, 4, 4)
+    LAYA_TILE(7, 256, 256, 2, 4, 1)
+    LAYA_TILE(8, 256, 128, 4, 2, 1)
+    LAYA_TILE(9, 128, 256, 2, 4, 1)
 #undef LAYA_TILE
     default: return hipErrorInvalidValue;
   }
@@ -237,6 +276,9 @@ hipError_t set_lds_attr() {
   LAYA_ATTR(256, 256, 2, 2, 1)
   LAYA_ATTR(256, 128, 2, 2, 1)
   LAYA_ATTR(128, 128, 2, 2, 2)
+  LAYA_ATTR(256, 256, 2, 4, 1)
+  LAYA_ATTR(256, 128, 4, 2, 1)
+  LAYA_ATTR(128, 256, 2, 4, 1)
 #undef LAYA_ATTR
   return e;
 }
@@ -264,7 +306,9 @@ hipError_t gemm_prepare() {
 void gemm_plan(int M, int N, int K, Epi epi, int cus, int* tile, int* splits) {
   // Largest tile that still gives every CU a workgroup; small problems fall back to small tiles
   // and, for the fp32 (split-K capable) epilogue, to K splits until the grid covers the chip.
-  const int order[] = {0, 1, 2, 3, 4, 5, 6};
+  // Eight-wave tiles first: with two waves per SIMD they sustain the most MFMA throughput when
+  // the grid is large enough; then four-wave tiles from large to small.
+  const int order[] = {7, 9, 8, 0, 1, 2, 3, 4, 5, 6};
   int best = 5, best_split = 1;
   for (int id : order) {
     const TileDef& d = kTiles[id];
@@ -289,8 +333,10 @@ void gemm_plan(int M, int N, int K, Epi epi, int cus, int* tile, int* splits) {
   *splits = best_split;
 }
 
-hipError_t launch_gemm(const GemmArgs& a, Epi epi, DType t, int tile, hipStream_t stream) {
+hipError_t launch_gemm(const GemmArgs& args, Epi epi, DType t, int tile, hipStream_t stream) {
   if (tile < 0 || tile >= kTileCount) return hipErrorInvalidValue;
+  GemmArgs a = args;
+  a.rows_major = a.M > a.N;
   if (a.M <= 0) return hipSuccess;
   if (a.K % BK || a.N % kTiles[tile].bn || a.splits < 1) return hipErrorInvalidValue;
   if (epi != Epi::F32 && a.splits != 1) return hipErrorInvalidValue;

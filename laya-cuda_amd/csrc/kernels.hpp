@@ -60,6 +60,7 @@ struct GemmArgs {
   void* k;
   void* vt;
   int width;
+  int rows_major;  // XCD share of the tile grid split by tile rows (A larger than B) or columns
 };
 
 struct GemmTile {

@@ -165,7 +165,7 @@ def linear(x, w, bias, out, kind, dtype, M, N, K, splits, tile):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("tile", range(7))
+@pytest.mark.parametrize("tile", range(10))
 def test_linear_tiles_match_fp32_product(gpu, dtype, tile):
     t = torch()
     rng = np.random.default_rng(tile)
@@ -221,7 +221,7 @@ def test_linear_gelu_epilogue(gpu, dtype):
     np.testing.assert_allclose(from16(out), expected, atol=tol, rtol=tol)
 
 
-@pytest.mark.parametrize("tile", [0, 2, 5, 6])
+@pytest.mark.parametrize("tile", [0, 2, 5, 6, 7, 9])
 def test_qkv_epilogue_writes_head_major_layout(gpu, tile):
     """Integer-valued operands make the product exact, so the layout check is bit-exact."""
     t = torch()
