@@ -138,14 +138,17 @@ int laya_abi_version(void);
  * (laya_cuda/ops.py:50-66; tests/test_gpu.py, tests/test_attention.py).
  * ------------------------------------------------------------------------------------------ */
 
-/* Attention work list for packed sequences: tiles of up to `block` query rows of one sequence,
- * plus zero-tiles for rows of no sequence; writes (row0,row1,seq) triples, returns the count
- * (or -1 if max_tiles is too small).  Host-only. */
+/* Attention work list for packed sequences (Slot.attend's ragged rows, runtime.py:82-88): tiles of
+ * up to `block` query rows of one sequence plus zero-tiles for rows of no sequence, as int32 quads
+ * (row0, row1, kstart, klen) with klen = -1 for zero-tiles; all max_tiles quads are written (unused
+ * ones as empty ranges).  Returns the used count, or -1 for a bad layout or too small a list.
+ * Host-only. */
 int laya_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_seq, int m, int block,
                          int32_t* tiles, int max_tiles);
 /* Query rows per tile of an attention kernel: mode 0 (K/V blocks staged once in LDS and shared by
- * `waves` waves of 32 queries each; large batches) -> 32*waves; mode 1 (one tile of 32 queries whose
- * keys are split across `waves` waves; batch-1 latency) -> 32.  -1 for an invalid pair. */
+ * `waves` = 1, 2, 4 or 8 waves of 32 queries each; large batches) -> 32*waves; mode 1 (one tile of
+ * 32 queries whose keys are split across `waves` = 2 or 4 waves; batch-1 latency) -> 32.  -1
+ * for an invalid pair. */
 int laya_attention_block(int mode, int waves);
 
 /* embed (kernels.cu:16-19) fused with the embeddings norm (runtime.py:93-95):
@@ -174,12 +177,11 @@ int laya_op_linear(const void* x, const void* w, const float* bias, void* out, i
 int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* k, void* vt,
                 int dtype16, int M, int width, int tile, void* stream);
 
-/* attention (kernels.cu:90-154, window -1) over a tile list from laya_attention_tiles built with
- * laya_attention_block(mode, waves) rows per tile. */
-int laya_op_attention(const void* q, const void* k, const void* vt, void* out,
-                      const int32_t* tiles, const int32_t* n_tiles, const int32_t* starts,
-                      const int32_t* lengths, int m, int heads, int max_tiles, int mode, int waves,
-                      int dtype16, void* stream);
+/* attention (kernels.cu:90-154, window -1) over a device copy (16-byte aligned) of a tile list from
+ * laya_attention_tiles built with laya_attention_block(mode, waves) rows per tile; q, k [heads][m][64],
+ * vt [heads][64][m], out [m][heads*64]. */
+int laya_op_attention(const void* q, const void* k, const void* vt, void* out, const int32_t* tiles,
+                      int m, int heads, int max_tiles, int mode, int waves, int dtype16, void* stream);
 
 #ifdef __cplusplus
 }

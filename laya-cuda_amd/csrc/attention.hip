@@ -10,7 +10,8 @@
 //   * one workgroup per (tile, head); a tile is a run of up to 32*NW query rows of ONE sequence,
 //     listed by the host so no tile straddles sequences (ragged batches waste no key blocks);
 //   * NW waves, each owning 32 queries; K and V^T blocks of 64 keys are staged through LDS,
-//     double-buffered, and shared by the waves;
+//     double-buffered, and shared by the waves (large batches), or - for batch-1 requests with few
+//     query tiles - the NW waves of a 32-query tile split the keys and merge their partial results;
 //   * the wave computes S^T = K Q^T with v_mfma_f32_32x32x16 (keys as rows, queries as
 //     columns).  In that accumulator layout a lane holds one query's scores for 16 keys, so
 //     the row softmax needs only one cross-lane exchange (lanes l and l^32), and the
@@ -24,80 +25,181 @@ namespace {
 
 constexpr int KB = 64;  // keys per block
 
-template <typename T, int NW>
-__global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
-  typedef typename Vec8<T>::type T8;
-  typedef typename Vec4<T>::type T4;
-  constexpr int NT = 64 * NW;
-  constexpr int CH = KB * 8 / NT;  // 16-byte chunks per thread per K (and per V) block
-
-  const int tile = blockIdx.x, head = blockIdx.y;
-  if (tile >= a.max_tiles || tile >= *a.n_tiles) return;
-  const int row0 = a.tiles[3 * tile], row1 = a.tiles[3 * tile + 1], seq = a.tiles[3 * tile + 2];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ld = a.heads * 64;
-  T* out = static_cast<T*>(a.out);
-
-  if (seq < 0) {  // rows that belong to no sequence: zeros (kernels.cu:102)
-    const int n = (row1 - row0) * 64;
-    for (int e = tid; e < n; e += NT) {
-      const int r = row0 + (e >> 6), c = e & 63;
-      out[static_cast<size_t>(r) * ld + head * 64 + c] = to_half<T>(0.f);
-    }
-    return;
-  }
-
-  const int start = a.starts[seq], len = a.lengths[seq], kend = start + len;
-  const int ql = lane & 31, g = lane >> 5;
-  const int q = row0 + wave * 32 + ql;
-  const bool qin = q < row1;
-  const bool qvalid = qin && q < kend;
-
-  const size_t plane = static_cast<size_t>(head) * a.m * 64;
-  const T* Q = static_cast<const T*>(a.q) + plane;
-  const T* K = static_cast<const T*>(a.k) + plane;
-  const T* Vt = static_cast<const T*>(a.vt) + plane;
-
-  // Q^T fragments for the four 16-wide head-dim steps: lane (g, q) holds Q[q][16ks + 8g + 0..7].
-  T8 qf[4];
+// One 64-key block of the single-pass softmax for this lane's query.  s holds the raw QK^T
+// scores of keys kb + 32kt + 8(r/4) + 4g + r%4 (the S^T accumulator layout); the running max
+// `mrow` is kept in the scaled log2 domain (x * log2(e) / 8), so each probability costs one FMA
+// and one exp2.  Keys at or past kend are masked only in the block that contains kend.  On
+// return s holds the block's unnormalised probabilities, lsum and o are rescaled.
+__device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], float& mrow, float& lsum, int kb,
+                                              int kend, int g) {
+  constexpr float c = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) in the exp2 domain
+  if (kb + KB > kend) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    if (qin) {
-      qf[ks] = *reinterpret_cast<const T8*>(Q + static_cast<size_t>(q) * 64 + 16 * ks + 8 * g);
-    } else {
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int s = 0; s < 8; ++s) qf[ks][s] = to_half<T>(0.f);
-    }
+      for (int r = 0; r < 16; ++r)
+        if (kb + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= kend) s[kt][r] = -INFINITY;
   }
+  float mx[4] = {s[0][0], s[0][1], s[0][2], s[0][3]};
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx[r & 3] = fmaxf(mx[r & 3], s[kt][r]);
+  float bmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+  const float mnew = fmaxf(mrow, bmax * c);
+  const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);  // first block: exp2(-inf) = 0
+  mrow = mnew;
+  float part[4] = {0.f, 0.f, 0.f, 0.f};  // four independent sums: a short dependency chain
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], c, -mnew));  // masked: exp2(-inf) = 0
+      s[kt][r] = p;
+      part[r & 3] += p;
+    }
+  lsum = lsum * alpha + ((part[0] + part[1]) + (part[2] + part[3]));
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+}
 
-  __shared__ __align__(16) T sK[2][KB * 64];
-  __shared__ __align__(16) T sV[2][64 * KB];
-
+// One 64-key block of K and V^T moved from HBM to LDS by NTH cooperating threads: global loads
+// are row-contiguous 16-byte chunks (8 lanes per 128-byte row), LDS rows are 128 bytes with the
+// chunk index XOR-swizzled by (row & 7).  V^T rows store keys permuted within each 16-key group
+// (logical keys 4g..4g+3 and 8+4g..8+4g+3 at physical 8g..8g+7) so that a lane's 16-byte read is
+// exactly the eight keys whose probabilities the S^T accumulator leaves in that lane.
+template <typename T, int NTH>
+struct KVStage {
+  static constexpr int CH = KB * 8 / NTH;  // 16-byte chunks per thread per K (and per V) block
+  static_assert(CH >= 1 && CH * NTH == KB * 8, "whole chunks per thread");
   i32x4 rk[CH], rv[CH];
-  auto gload = [&](int kb) {
+
+  // Rows past the end of the slot are read from its last row instead (branch-free loads): such keys
+  // lie past the end of every sequence, so the softmax gives them probability exactly 0, and the
+  // rows they read are finite values of this slot.
+  __device__ __forceinline__ void load(const T* K, const T* Vt, int m, int kb, int tid) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
-      const int c = tid + NT * i, r = c >> 3, u = c & 7;
-      const int key = kb + r;
-      rk[i] = key < a.m ? *reinterpret_cast<const i32x4*>(K + static_cast<size_t>(key) * 64 + u * 8) : i32x4{0, 0, 0, 0};
-      const int k8 = kb + u * 8;  // V^T row r = head dim, keys k8..k8+7
-      rv[i] = k8 < a.m ? *reinterpret_cast<const i32x4*>(Vt + static_cast<size_t>(r) * a.m + k8) : i32x4{0, 0, 0, 0};
+      const int c = tid + NTH * i, r = c >> 3, u = c & 7;
+      const int key = min(kb + r, m - 1);
+      rk[i] = *reinterpret_cast<const i32x4*>(K + static_cast<size_t>(key) * 64 + u * 8);
+      const int k8 = min(kb + u * 8, m - 8);  // V^T row r = head dim, keys k8..k8+7
+      rv[i] = *reinterpret_cast<const i32x4*>(Vt + static_cast<size_t>(r) * m + k8);
     }
-  };
-  auto lstore = [&](int buf) {
+  }
+  __device__ __forceinline__ void store(T* sK, T* sV, int tid) const {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
-      const int c = tid + NT * i, r = c >> 3, u = c & 7;
-      *reinterpret_cast<i32x4*>(&sK[buf][r * 64 + ((u ^ (r & 7)) << 3)]) = rk[i];
-      // Keys 8u..8u+7 of V^T row r: group cg = u/2, half = u%2.  Logical keys 4g..4g+3 and
-      // 8+4g..8+4g+3 of a 16-key group must sit at physical 8g..8g+7 (one 16-byte read per lane).
-      const int cg = u >> 1, half = u & 1;
-      T* vrow = &sV[buf][r * KB];
+      const int c = tid + NTH * i, r = c >> 3, u = c & 7;
+      *reinterpret_cast<i32x4*>(sK + r * 64 + ((u ^ (r & 7)) << 3)) = rk[i];
+      const int cg = u >> 1, half = u & 1;  // keys 8u..8u+7 = half `half` of 16-key group cg
+      T* vrow = sV + r * KB;
       const int p0 = ((2 * cg) ^ (r & 7)) << 3, p1 = ((2 * cg + 1) ^ (r & 7)) << 3;
       *reinterpret_cast<int2*>(vrow + p0 + 4 * half) = make_int2(rv[i][0], rv[i][1]);
       *reinterpret_cast<int2*>(vrow + p1 + 4 * half) = make_int2(rv[i][2], rv[i][3]);
     }
-  };
+  }
+};
+
+// One wave's work on one LDS-resident 64-key block for its 32 queries: S^T = K Q^T
+// (v_mfma_f32_32x32x16: keys as rows, queries as columns, so a lane holds one query's scores for
+// 16 keys), the online-softmax step, and O^T += V^T P^T with P straight from registers.
+template <typename T>
+__device__ __forceinline__ void attend_block(const T* sK, const T* sV, const typename Vec8<T>::type (&qf)[4],
+                                             f32x16 (&o)[2], float& mrow, float& lsum, int kb, int kend, int lane) {
+  typedef typename Vec8<T>::type T8;
+  const int ql = lane & 31, g = lane >> 5;
+  f32x16 s[2];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
+    const int kr = kt * 32 + ql;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int ch = 2 * ks + g;
+      const T8 kf = *reinterpret_cast<const T8*>(sK + kr * 64 + ((ch ^ (kr & 7)) << 3));
+      s[kt] = mfma32(kf, qf[ks], s[kt]);
+    }
+  }
+  softmax_block(s, o, mrow, lsum, kb, kend, g);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    T8 pb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pb[e] = to_half<T>(s[c >> 1][8 * (c & 1) + e]);
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const int vr = d * 32 + ql;
+      const T8 vf = *reinterpret_cast<const T8*>(sV + vr * KB + (((2 * c + g) ^ (vr & 7)) << 3));
+      o[d] = mfma32(vf, pb, o[d]);
+    }
+  }
+}
+
+// Rows of no sequence (span padding, rows past the last sequence) are exact zeros (kernels.cu:102).
+template <typename T>
+__device__ __forceinline__ void zero_rows(T* out, int ld, int head, int row0, int row1, int tid, int nt) {
+  const int n = (row1 - row0) * 64;
+  for (int e = tid; e < n; e += nt) {
+    const int r = row0 + (e >> 6), c = e & 63;
+    out[static_cast<size_t>(r) * ld + head * 64 + c] = to_half<T>(0.f);
+  }
+}
+
+// Q^T fragments for the four 16-wide head-dim steps: lane (g, q) holds Q[q][16ks + 8g + 0..7].
+template <typename T>
+__device__ __forceinline__ void load_q(const T* Q, int q, bool qin, int g, typename Vec8<T>::type (&qf)[4]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    if (qin) {
+      qf[ks] = *reinterpret_cast<const typename Vec8<T>::type*>(Q + static_cast<size_t>(q) * 64 + 16 * ks + 8 * g);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[ks][e] = to_half<T>(0.f);
+    }
+  }
+}
+
+// Large batches: a workgroup of NW waves owns 32*NW queries of one sequence and one head; every
+// K/V block is staged once in LDS (double-buffered, the next block's global loads in flight during
+// the current block's MFMAs) and shared by all NW waves.
+template <typename T, int NW>
+__device__ __forceinline__ void attention_shared(const AttnArgs& a) {
+  typedef typename Vec8<T>::type T8;
+  typedef typename Vec4<T>::type T4;
+  constexpr int NT = 64 * NW;
+
+  const int tile = blockIdx.x, head = blockIdx.y;
+  if (tile >= a.max_tiles) return;
+  const int4 td = reinterpret_cast<const int4*>(a.tiles)[tile];
+  const int row0 = td.x, row1 = td.y, start = td.z, len = td.w;
+  if (row0 >= row1) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ld = a.heads * 64;
+  T* out = static_cast<T*>(a.out);
+  if (len < 0) {
+    zero_rows(out, ld, head, row0, row1, tid, NT);
+    return;
+  }
+
+  const int kend = start + len;
+  const int ql = lane & 31, g = lane >> 5;
+  const int q = row0 + wave * 32 + ql;
+  const bool qin = q < row1;
+  const bool qvalid = qin && q < kend;
+  const size_t plane = static_cast<size_t>(head) * a.m * 64;
+  const T* K = static_cast<const T*>(a.k) + plane;
+  const T* Vt = static_cast<const T*>(a.vt) + plane;
+  T8 qf[4];
+  load_q(static_cast<const T*>(a.q) + plane, q, qin, g, qf);
+
+  __shared__ __align__(16) T sK[2][KB * 64];
+  __shared__ __align__(16) T sV[2][64 * KB];
+  KVStage<T, NT> st;
 
   f32x16 o[2];
 #pragma unroll
@@ -105,74 +207,16 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[d][r] = 0.f;
   float mrow = -INFINITY, lsum = 0.f;
-  const float scale = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) in the exp2 domain
 
   const int nkb = (len + KB - 1) / KB;
-  gload(start);
-  lstore(0);
+  st.load(K, Vt, a.m, start, tid);
+  st.store(sK[0], sV[0], tid);
   __syncthreads();
   for (int j = 0; j < nkb; ++j) {
     const int cur = j & 1, kb = start + j * KB;
-    if (j + 1 < nkb) gload(kb + KB);
-
-    // S^T for keys kb..kb+63 (two 32-key tiles) against this wave's 32 queries.
-    f32x16 s[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
-      const int kr = kt * 32 + ql;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int ch = 2 * ks + g;
-        const T8 kf = *reinterpret_cast<const T8*>(&sK[cur][kr * 64 + ((ch ^ (kr & 7)) << 3)]);
-        s[kt] = mfma32(kf, qf[ks], s[kt]);
-      }
-    }
-    // Mask keys past the sequence, scale, and take this block's max per query.
-    float bmax = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        const float x = key < kend ? s[kt][r] * scale : -INFINITY;
-        s[kt][r] = x;
-        bmax = fmaxf(bmax, x);
-      }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    const float mnew = fmaxf(mrow, bmax);
-    const float alpha = mrow == -INFINITY ? 0.f : exp2f(mrow - mnew);
-    mrow = mnew;
-    float psum = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = s[kt][r] == -INFINITY ? 0.f : exp2f(s[kt][r] - mnew);
-        s[kt][r] = p;
-        psum += p;
-      }
-    lsum = lsum * alpha + psum;
-#pragma unroll
-    for (int d = 0; d < 2; ++d)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
-
-    // O^T += V^T P^T over four 16-key chunks.
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      T8 pb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pb[e] = to_half<T>(s[c >> 1][8 * (c & 1) + e]);
-#pragma unroll
-      for (int d = 0; d < 2; ++d) {
-        const int vr = d * 32 + ql;
-        const T8 vf = *reinterpret_cast<const T8*>(&sV[cur][vr * KB + (((2 * c + g) ^ (vr & 7)) << 3)]);
-        o[d] = mfma32(vf, pb, o[d]);
-      }
-    }
-    if (j + 1 < nkb) lstore(cur ^ 1);
+    if (j + 1 < nkb) st.load(K, Vt, a.m, kb + KB, tid);
+    attend_block<T>(sK[cur], sV[cur], qf, o, mrow, lsum, kb, kend, lane);
+    if (j + 1 < nkb) st.store(sK[cur ^ 1], sV[cur ^ 1], tid);
     __syncthreads();
   }
 
@@ -191,101 +235,58 @@ __global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
     }
 }
 
-// Split-key variant for small batches (few query tiles): a workgroup owns 32 queries of one
-// sequence and one head, and its NW waves split that sequence's 64-key blocks (wave w takes
-// blocks w, w+NW, ...).  Each wave reads its K and V^T fragments straight from global memory into
-// MFMA operand registers (no reuse between waves, so no LDS staging) and prefetches its next block
-// while computing the current one; the serial chain per wave is ceil(blocks / NW) instead of
-// blocks.  The NW partial (max, sum, O) triples are merged through LDS at the end.
+template <typename T, int NW>
+__global__ __launch_bounds__(64 * NW) void attention_kernel(AttnArgs a) {
+  attention_shared<T, NW>(a);
+}
+// Eight waves: capped at 128 VGPRs so that two 512-thread workgroups share a CU.
+template <typename T>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void attention_kernel8(AttnArgs a) {
+  attention_shared<T, 8>(a);
+}
+
+// Small batches (few query tiles): a workgroup owns 32 queries of one sequence and one head, and
+// its NW waves split that sequence's 64-key blocks (wave w takes blocks w, w+NW, ...), so the
+// serial chain per wave is ceil(blocks / NW) instead of blocks.  Each wave stages its own blocks
+// through its own double-buffered LDS region with coalesced loads (the next one in flight while
+// it computes the current one); the NW partial (max, sum, O) triples are merged through LDS.
 template <typename T, int NW>
 __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
   typedef typename Vec8<T>::type T8;
   typedef typename Vec4<T>::type T4;
   constexpr int NT = 64 * NW;
   constexpr int OP = 65;  // LDS pitch of a merged query row (floats): conflict-free column writes
+  constexpr int STAGE = 2 * 2 * KB * 64;  // per wave: two buffers of K and V^T (16-bit elements)
 
   const int tile = blockIdx.x, head = blockIdx.y;
-  if (tile >= a.max_tiles || tile >= *a.n_tiles) return;
-  const int row0 = a.tiles[3 * tile], row1 = a.tiles[3 * tile + 1], seq = a.tiles[3 * tile + 2];
+  if (tile >= a.max_tiles) return;
+  const int4 td = reinterpret_cast<const int4*>(a.tiles)[tile];
+  const int row0 = td.x, row1 = td.y, start = td.z, len = td.w;
+  if (row0 >= row1) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ld = a.heads * 64;
   T* out = static_cast<T*>(a.out);
-
-  if (seq < 0) {  // rows that belong to no sequence: zeros (kernels.cu:102)
-    const int n = (row1 - row0) * 64;
-    for (int e = tid; e < n; e += NT) {
-      const int r = row0 + (e >> 6), c = e & 63;
-      out[static_cast<size_t>(r) * ld + head * 64 + c] = to_half<T>(0.f);
-    }
+  if (len < 0) {
+    zero_rows(out, ld, head, row0, row1, tid, NT);
     return;
   }
 
-  const int start = a.starts[seq], len = a.lengths[seq], kend = start + len;
+  const int kend = start + len;
   const int ql = lane & 31, g = lane >> 5;
   const int q = row0 + ql;
   const bool qin = q < row1;
   const size_t plane = static_cast<size_t>(head) * a.m * 64;
-  const T* Q = static_cast<const T*>(a.q) + plane;
   const T* K = static_cast<const T*>(a.k) + plane;
   const T* Vt = static_cast<const T*>(a.vt) + plane;
-
   T8 qf[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    if (qin) {
-      qf[ks] = *reinterpret_cast<const T8*>(Q + static_cast<size_t>(q) * 64 + 16 * ks + 8 * g);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[ks][e] = to_half<T>(0.f);
-    }
-  }
+  load_q(static_cast<const T*>(a.q) + plane, q, qin, g, qf);
 
-  // Fragments of one 64-key block.  K (A operand of S^T = K Q^T): lane (ql, g) holds key
-  // kb + 32kt + ql, dims 16ks + 8g..+7.  V^T (A operand of O^T = V^T P^T): lane holds head dim
-  // 32d + ql and, of the 16-key chunk c, keys 4g..4g+3 and 8+4g..8+4g+3 - the keys whose
-  // probabilities the S^T accumulator leaves in this lane.
-  T8 kf[2][4], vf[4][2];
-  auto load_block = [&](int kb, T8 (&kfr)[2][4], T8 (&vfr)[4][2]) {
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int key = kb + 32 * kt + ql;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (key < a.m) {
-          kfr[kt][ks] = *reinterpret_cast<const T8*>(K + static_cast<size_t>(key) * 64 + 16 * ks + 8 * g);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) kfr[kt][ks][e] = to_half<T>(0.f);
-        }
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int k0 = kb + 16 * c + 4 * g, k1 = k0 + 8;
-#pragma unroll
-      for (int d = 0; d < 2; ++d) {
-        const T* row = Vt + static_cast<size_t>(32 * d + ql) * a.m;
-        T4 lo, hi;
-        if (k0 < a.m) {
-          lo = *reinterpret_cast<const T4*>(row + k0);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) lo[e] = to_half<T>(0.f);
-        }
-        if (k1 < a.m) {
-          hi = *reinterpret_cast<const T4*>(row + k1);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) hi[e] = to_half<T>(0.f);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          vfr[c][d][e] = lo[e];
-          vfr[c][d][4 + e] = hi[e];
-        }
-      }
-    }
-  };
+  // Staging area during the key loop, merge area after it.
+  static_assert(NW * STAGE * sizeof(T) >= NW * 32 * OP * sizeof(float), "merge area fits the staging area");
+  __shared__ __align__(16) T lds[NW * STAGE];
+  __shared__ float sM[NW][32], sL[NW][32];
+  T* mine = lds + wave * STAGE;
+  KVStage<T, 64> st;
 
   f32x16 o[2];
 #pragma unroll
@@ -293,72 +294,21 @@ __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[d][r] = 0.f;
   float mrow = -INFINITY, lsum = 0.f;
-  const float scale = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) in the exp2 domain
 
-  const int nkb = (len + 63) / 64;
-  T8 kn[2][4], vn[4][2];
-  if (wave < nkb) load_block(start + 64 * wave, kn, vn);
-  for (int j = wave; j < nkb; j += NW) {
-    const int kb = start + 64 * j;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kf[kt][ks] = kn[kt][ks];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int d = 0; d < 2; ++d) vf[c][d] = vn[c][d];
-    if (j + NW < nkb) load_block(kb + 64 * NW, kn, vn);
-
-    f32x16 s[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) s[kt] = mfma32(kf[kt][ks], qf[ks], s[kt]);
-    }
-    float bmax = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        const float x = key < kend ? s[kt][r] * scale : -INFINITY;
-        s[kt][r] = x;
-        bmax = fmaxf(bmax, x);
-      }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    const float mnew = fmaxf(mrow, bmax);
-    const float alpha = mrow == -INFINITY ? 0.f : exp2f(mrow - mnew);
-    mrow = mnew;
-    float psum = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = s[kt][r] == -INFINITY ? 0.f : exp2f(s[kt][r] - mnew);
-        s[kt][r] = p;
-        psum += p;
-      }
-    lsum = lsum * alpha + psum;
-#pragma unroll
-    for (int d = 0; d < 2; ++d)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      T8 pb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pb[e] = to_half<T>(s[c >> 1][8 * (c & 1) + e]);
-#pragma unroll
-      for (int d = 0; d < 2; ++d) o[d] = mfma32(vf[c][d], pb, o[d]);
-    }
+  // LDS accesses of one wave execute in issue order, so a wave's own staging needs no barrier.
+  const int nkb = (len + KB - 1) / KB;
+  if (wave < nkb) st.load(K, Vt, a.m, start + KB * wave, lane);
+  for (int j = wave, it = 0; j < nkb; j += NW, ++it) {
+    T* sK = mine + (it & 1) * 2 * KB * 64;
+    T* sV = sK + KB * 64;
+    st.store(sK, sV, lane);
+    if (j + NW < nkb) st.load(K, Vt, a.m, start + KB * (j + NW), lane);
+    attend_block<T>(sK, sV, qf, o, mrow, lsum, start + KB * j, kend, lane);
   }
 
   // Merge the waves' partial results: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w.
-  __shared__ float sO[NW][32 * OP];
-  __shared__ float sM[NW][32], sL[NW][32];
+  __syncthreads();  // every wave is done with the staging area
+  float* sO = reinterpret_cast<float*>(lds) + wave * 32 * OP;
   const float ltot = lsum + __shfl_xor(lsum, 32, 64);
   if (g == 0) {
     sM[wave][ql] = mrow;
@@ -367,7 +317,7 @@ __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
 #pragma unroll
   for (int d = 0; d < 2; ++d)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sO[wave][ql * OP + 32 * d + 8 * (r >> 2) + 4 * g + (r & 3)] = o[d][r];
+    for (int r = 0; r < 16; ++r) sO[ql * OP + 32 * d + 8 * (r >> 2) + 4 * g + (r & 3)] = o[d][r];
   __syncthreads();
 
   constexpr int DPT = 64 * 32 / NT;  // head dims per thread in the merge
@@ -380,11 +330,12 @@ __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
   float wt[NW], total = 0.f;
 #pragma unroll
   for (int w = 0; w < NW; ++w) {
-    wt[w] = sM[w][mq] == -INFINITY ? 0.f : exp2f(sM[w][mq] - mx);
+    wt[w] = __builtin_amdgcn_exp2f(sM[w][mq] - mx);  // a wave with no block: exp2(-inf) = 0
     total += wt[w] * sL[w][mq];
   }
   const bool valid = qo < kend && total > 0.f;
   const float inv = valid ? 1.0f / total : 0.f;
+  const float* merged = reinterpret_cast<const float*>(lds);
   T* orow = out + static_cast<size_t>(qo) * ld + head * 64 + d0;
 #pragma unroll
   for (int e = 0; e < DPT; e += 4) {
@@ -393,7 +344,7 @@ __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
     for (int i = 0; i < 4; ++i) {
       float acc = 0.f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) acc += wt[w] * sO[w][mq * OP + d0 + e + i];
+      for (int w = 0; w < NW; ++w) acc += wt[w] * merged[w * 32 * OP + mq * OP + d0 + e + i];
       v[i] = to_half<T>(valid ? acc * inv : 0.f);
     }
     *reinterpret_cast<T4*>(orow + e) = v;
@@ -407,7 +358,6 @@ hipError_t launch_t(const AttnArgs& a, int mode, int waves, hipStream_t stream) 
     switch (waves) {
       case 2: hipLaunchKernelGGL((attention_split_kernel<T, 2>), grid, dim3(128), 0, stream, a); break;
       case 4: hipLaunchKernelGGL((attention_split_kernel<T, 4>), grid, dim3(256), 0, stream, a); break;
-      case 8: hipLaunchKernelGGL((attention_split_kernel<T, 8>), grid, dim3(512), 0, stream, a); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -416,6 +366,7 @@ hipError_t launch_t(const AttnArgs& a, int mode, int waves, hipStream_t stream) 
     case 1: hipLaunchKernelGGL((attention_kernel<T, 1>), grid, dim3(64), 0, stream, a); break;
     case 2: hipLaunchKernelGGL((attention_kernel<T, 2>), grid, dim3(128), 0, stream, a); break;
     case 4: hipLaunchKernelGGL((attention_kernel<T, 4>), grid, dim3(256), 0, stream, a); break;
+    case 8: hipLaunchKernelGGL((attention_kernel8<T>), grid, dim3(512), 0, stream, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -425,9 +376,43 @@ hipError_t launch_t(const AttnArgs& a, int mode, int waves, hipStream_t stream) 
 
 int attention_block_rows(int mode, int waves) { return mode == kAttnSplitKeys ? 32 : 32 * waves; }
 
+int build_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_seq, int m, int block,
+                          int32_t* tiles, int max_tiles) {
+  if (block <= 0 || block % 16 || max_tiles < 0) return -1;
+  int nt = 0, row = 0;
+  auto put = [&](int r0, int r1, int kstart, int klen) {
+    if (nt >= max_tiles) return false;
+    tiles[4 * nt] = r0;
+    tiles[4 * nt + 1] = r1;
+    tiles[4 * nt + 2] = kstart;
+    tiles[4 * nt + 3] = klen;
+    ++nt;
+    return true;
+  };
+  auto run = [&](int upto, int kstart, int klen) {
+    while (row < upto) {
+      const int r1 = (upto - row > block) ? row + block : upto;
+      if (!put(row, r1, kstart, klen)) return false;
+      row = r1;
+    }
+    return true;
+  };
+  for (int s = 0; s < n_seq; ++s) {
+    const int st = starts[s], len = lengths[s], e = st + (len + 15) / 16 * 16;
+    if (st % 16 || st < row || len < 0 || e > m) return -1;
+    if (!run(st, 0, -1) || !run(e, st, len)) return -1;
+  }
+  if (!run(m, 0, -1)) return -1;
+  for (int t = nt; t < max_tiles; ++t) {
+    tiles[4 * t] = tiles[4 * t + 1] = tiles[4 * t + 2] = 0;
+    tiles[4 * t + 3] = -1;
+  }
+  return nt;
+}
+
 bool attention_mode_valid(int mode, int waves) {
-  if (mode == kAttnSharedKV) return waves == 1 || waves == 2 || waves == 4;
-  if (mode == kAttnSplitKeys) return waves == 2 || waves == 4 || waves == 8;
+  if (mode == kAttnSharedKV) return waves == 1 || waves == 2 || waves == 4 || waves == 8;
+  if (mode == kAttnSplitKeys) return waves == 2 || waves == 4;
   return false;
 }
 

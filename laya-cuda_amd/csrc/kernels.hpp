@@ -75,17 +75,21 @@ hipError_t launch_gemm(const GemmArgs& a, Epi epi, DType t, int tile, hipStream_
 
 // ---- fused bidirectional attention over packed rows ----
 // tiles: [max_tiles][3] = (row0, row1, seq); seq < 0 marks rows to zero.
+// Attention work list entry (16-byte aligned int4): query rows [row0, row1) of one sequence whose
+// keys are rows [kstart, kstart + klen); klen < 0 marks rows of no sequence (written as zeros), and
+// row0 == row1 an unused entry.
 struct AttnArgs {
   const void* q;   // [heads][m][64]
   const void* k;   // [heads][m][64]
   const void* vt;  // [heads][64][m]
   void* out;       // [m][heads*64]
-  const int32_t* tiles;
-  const int32_t* n_tiles;
-  const int32_t* starts;
-  const int32_t* lengths;
+  const int32_t* tiles;  // [max_tiles][4] = (row0, row1, kstart, klen)
   int m, heads, max_tiles;
 };
+// Host: tile list of packed sequences (starts multiples of 16, increasing, spans of 16) with at
+// most `block` query rows per tile; fills all max_tiles entries, returns the used count or -1.
+int build_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_seq, int m, int block,
+                          int32_t* tiles, int max_tiles);
 // Attention kernels: kAttnSharedKV - a workgroup of `waves` waves owns 32*waves queries and stages
 // each K/V block once in LDS for all of them (large batches); kAttnSplitKeys - a workgroup owns 32
 // queries and its `waves` waves split the keys, merging at the end (few query tiles: batch 1).

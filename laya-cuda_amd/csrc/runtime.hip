@@ -96,13 +96,14 @@ struct Expected {
 // derived work lists the host builds before the single upload.
 struct Layout {
   size_t meta, ids, positions, rows, kinds, starts, lengths, counts, qkind, indices, user_end;
-  size_t qoff, tiles, n_tiles, sel_src, sel_q, n_sel, total;
+  size_t qoff, tiles, sel_src, sel_q, n_sel, total;
   int T, R;
 };
 Layout make_layout(int m, int b, int k) {
   Layout L{};
   size_t o = 0;
   auto take = [&](size_t n) { size_t at = o; o += n; return at; };
+  auto take16 = [&](size_t n) { o = (o + 3) / 4 * 4; return take(n); };  // 16-byte aligned
   L.meta = take(4);
   L.ids = take(m);
   L.positions = take(m);
@@ -117,8 +118,7 @@ Layout make_layout(int m, int b, int k) {
   L.T = m / 16;
   L.R = b * (k + 1);
   L.qoff = take(b);
-  L.tiles = take(static_cast<size_t>(3) * L.T);
-  L.n_tiles = take(1);
+  L.tiles = take16(static_cast<size_t>(4) * L.T);
   L.sel_src = take(L.R);
   L.sel_q = take(L.R);
   L.n_sel = take(1);
@@ -266,10 +266,12 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
     // sharing LDS-staged keys between query tiles, so the serial key loop is short.
     if (static_cast<long long>(m / 128) * c.heads >= 2LL * E.cus) {
       s->attn_mode = kAttnSharedKV;
-      s->attn_waves = 4;
+      s->attn_waves = 8;
     } else {
+      // Two waves per 32-query tile: measured faster than four at 512 and 1,024 keys (the extra
+      // waves cost more in LDS staging and merging than they save in serial key blocks).
       s->attn_mode = kAttnSplitKeys;
-      s->attn_waves = 4;
+      s->attn_waves = 2;
     }
     s->head_splits = head_gemm_splits(s->L.R, d, d, E.cus);
     s->act_splits = head_gemm_splits(b, c.act_hidden, E.act_k, E.cus);
@@ -336,37 +338,14 @@ void derive_inputs(const Engine& E, Slot& s) {
     LAYA_REQUIRE(P[L.positions + i] >= 0 && P[L.positions + i] < c.max_positions, "position out of range");
   }
   // Attention tiles: sequences in increasing start order, 16-aligned, non-overlapping.
-  const int block = attention_block_rows(s.attn_mode, s.attn_waves);
-  int32_t* tiles = P + L.tiles;
-  int nt = 0, row = 0;
-  auto zero_to = [&](int upto) {
-    while (row < upto) {
-      const int r1 = (upto - row > block) ? row + block : upto;
-      tiles[3 * nt] = row;
-      tiles[3 * nt + 1] = r1;
-      tiles[3 * nt + 2] = -1;
-      ++nt;
-      row = r1;
-    }
-  };
   for (int sq = 0; sq < n_seq; ++sq) {
     const int st = P[L.starts + sq], len = P[L.lengths + sq];
-    LAYA_REQUIRE(st % 16 == 0 && st >= row && len >= 0 && st + span16(len) <= m,
+    LAYA_REQUIRE(st % 16 == 0 && len >= 0 && st + span16(len) <= m && (sq == 0 || st >= P[L.starts + sq - 1] + span16(P[L.lengths + sq - 1])),
                  "sequences must start at increasing multiples of 16 rows and fit the shape class");
-    zero_to(st);
-    const int e = st + span16(len);
-    while (row < e) {
-      const int r1 = (e - row > block) ? row + block : e;
-      tiles[3 * nt] = row;
-      tiles[3 * nt + 1] = r1;
-      tiles[3 * nt + 2] = sq;
-      ++nt;
-      row = r1;
-    }
   }
-  zero_to(m);
-  LAYA_REQUIRE(nt <= L.T, "attention tile list overflow");
-  P[L.n_tiles] = nt;
+  const int nt = build_attention_tiles(P + L.starts, P + L.lengths, n_seq, m,
+                                       attention_block_rows(s.attn_mode, s.attn_waves), P + L.tiles, L.T);
+  LAYA_REQUIRE(nt >= 0, "attention tile list overflow");
   // Compact head rows: per question its CLS row then its option rows.
   int ns = 0;
   for (int q = 0; q < n_q; ++q) {
@@ -424,7 +403,7 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       check_launch(launch_gemm(g, Epi::QKV, t, s.tile[0], st), "qkv");
       break;
     case kAttention: {
-      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, P + L.n_tiles, P + L.starts, P + L.lengths, m, c.heads, L.T};
+      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, m, c.heads, L.T};
       check_launch(launch_attention(aa, t, s.attn_mode, s.attn_waves, st), "attention");
       break;
     }
@@ -871,31 +850,8 @@ int laya_attention_block(int mode, int waves) {
 
 int laya_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_seq, int m, int block, int32_t* tiles,
                          int max_tiles) {
-  int nt = 0, row = 0;
-  auto put = [&](int r0, int r1, int sq) {
-    if (nt >= max_tiles) return false;
-    tiles[3 * nt] = r0;
-    tiles[3 * nt + 1] = r1;
-    tiles[3 * nt + 2] = sq;
-    ++nt;
-    return true;
-  };
-  auto run = [&](int upto, int sq) {
-    while (row < upto) {
-      const int r1 = (upto - row > block) ? row + block : upto;
-      if (!put(row, r1, sq)) return false;
-      row = r1;
-    }
-    return true;
-  };
-  if (block <= 0 || block % 16) return -1;
-  for (int s = 0; s < n_seq; ++s) {
-    const int st = starts[s], e = st + span16(lengths[s]);
-    if (st % 16 || st < row || e > m) return -1;
-    if (!run(st, -1) || !run(e, s)) return -1;
-  }
-  if (!run(m, -1)) return -1;
-  return nt;
+  if (!starts || !lengths || !tiles || n_seq < 0) return -1;
+  return build_attention_tiles(starts, lengths, n_seq, m, block, tiles, max_tiles);
 }
 
 static DType half_type(int dtype16) { return dtype16 == LAYA_F16 ? DType::F16 : DType::BF16; }
@@ -955,14 +911,14 @@ int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* 
   });
 }
 
-int laya_op_attention(const void* q, const void* k, const void* vt, void* out, const int32_t* tiles,
-                      const int32_t* n_tiles, const int32_t* starts, const int32_t* lengths, int m, int heads,
-                      int max_tiles, int mode, int waves, int dtype16, void* stream) {
+int laya_op_attention(const void* q, const void* k, const void* vt, void* out, const int32_t* tiles, int m,
+                      int heads, int max_tiles, int mode, int waves, int dtype16, void* stream) {
   return guarded(nullptr, [&] {
     LAYA_REQUIRE(attention_mode_valid(mode, waves),
-                 "mode 0 (shared K/V) takes 1, 2 or 4 waves; mode 1 (split keys) takes 2, 4 or 8");
+                 "mode 0 (shared K/V) takes 1, 2, 4 or 8 waves; mode 1 (split keys) takes 2 or 4");
     LAYA_REQUIRE(m % 16 == 0, "rows must be a multiple of 16");
-    AttnArgs a{q, k, vt, out, tiles, n_tiles, starts, lengths, m, heads, max_tiles};
+    LAYA_REQUIRE((reinterpret_cast<uintptr_t>(tiles) & 15) == 0, "tile list must be 16-byte aligned");
+    AttnArgs a{q, k, vt, out, tiles, m, heads, max_tiles};
     check_launch(launch_attention(a, half_type(dtype16), mode, waves, static_cast<hipStream_t>(stream)),
                  "attention");
   });

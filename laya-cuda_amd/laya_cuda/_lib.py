@@ -56,7 +56,7 @@ SIGNATURES = {
     "laya_op_norm": ([_p, _p, _i, _i64, _p, _p, _p, _f, _p, _p, _p, _i, _i, _i, _p], _i),
     "laya_op_linear": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p], _i),
     "laya_op_qkv": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p], _i),
-    "laya_op_attention": ([_p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p], _i),
+    "laya_op_attention": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p], _i),
 }
 
 _lib = None

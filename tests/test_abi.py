@@ -45,11 +45,14 @@ def test_packed_block_size_matches_the_python_packer():
 def tiles(starts, lengths, m, block, max_tiles=None):
     lib = _lib.load()
     max_tiles = max_tiles or m // 16
-    out = np.zeros(3 * max_tiles, np.int32)
+    out = np.full(4 * max_tiles, 7, np.int32)
     s, n = np.asarray(starts, np.int32), np.asarray(lengths, np.int32)
     count = lib.laya_attention_tiles(s.ctypes.data_as(ct.POINTER(ct.c_int32)), n.ctypes.data_as(ct.POINTER(ct.c_int32)),
                                      len(s), m, block, out.ctypes.data_as(ct.POINTER(ct.c_int32)), max_tiles)
-    return count, out[:3 * max(count, 0)].reshape(-1, 3)
+    quads = out.reshape(-1, 4)
+    if count >= 0:  # every entry past the used ones is an empty range
+        assert (quads[count:, 0] == quads[count:, 1]).all() and (quads[count:, 3] == -1).all()
+    return count, quads[:max(count, 0)]
 
 
 @pytest.mark.parametrize("block", [32, 64, 128])
@@ -63,13 +66,15 @@ def test_attention_tiles_cover_every_row_once(block):
     count, t = tiles(starts, lengths, m, block)
     assert count > 0
     covered = np.zeros(m, int)
-    for r0, r1, seq in t:
+    for r0, r1, kstart, klen in t:
         assert 0 < r1 - r0 <= block
         covered[r0:r1] += 1
-        if seq >= 0:  # a tile never straddles a sequence's span
-            assert starts[seq] <= r0 and r1 <= starts[seq] + -(-lengths[seq] // 16) * 16
+        if klen >= 0:  # a tile never straddles a sequence's span, and carries that sequence's keys
+            seq = starts.index(kstart)
+            assert klen == lengths[seq]
+            assert kstart <= r0 and r1 <= kstart + -(-klen // 16) * 16
     assert (covered == 1).all()
-    assert (t[:, 2] == -1).sum() >= 1  # rows past the last sequence are zero tiles
+    assert (t[:, 3] == -1).sum() >= 1  # rows past the last sequence are zero tiles
 
 
 def test_attention_tiles_reject_bad_layouts():

@@ -250,7 +250,7 @@ def span(n):
     return -(-n // 16) * 16
 
 
-@pytest.mark.parametrize("mode,waves", [(0, 1), (0, 2), (0, 4), (1, 2), (1, 4), (1, 8)])
+@pytest.mark.parametrize("mode,waves", [(0, 1), (0, 2), (0, 4), (0, 8), (1, 2), (1, 4)])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("lengths", [[32], [7, 96], [128, 1], [250, 131], [256, 219, 145], [500], [1024, 333]])
 def test_packed_attention_matches_float64(gpu, lengths, dtype, mode, waves):
@@ -267,14 +267,13 @@ def test_packed_attention_matches_float64(gpu, lengths, dtype, mode, waves):
     vt = x[:, 2].transpose(1, 2, 0).copy()             # [h][64][m]
     max_tiles = m // 16
     block = lib.laya_attention_block(mode, waves)
-    tiles = np.zeros(3 * max_tiles, np.int32)
+    tiles = np.zeros(4 * max_tiles, np.int32)
     lens = np.asarray(lengths, np.int32)
     n = lib.laya_attention_tiles(starts.ctypes.data_as(ct.POINTER(ct.c_int32)), lens.ctypes.data_as(ct.POINTER(ct.c_int32)),
                                  len(lengths), m, block, tiles.ctypes.data_as(ct.POINTER(ct.c_int32)), max_tiles)
     assert n > 0
     out = t.full((m, h * 64), float("nan"), dtype=t.float16 if dtype == "f16" else t.bfloat16, device=gpu)
-    args = [to16(a, dtype, gpu) for a in (q, k, vt)] + [out] + [dev(a, gpu) for a in (tiles, np.array([n], np.int32),
-                                                                                       starts, lens)]
+    args = [to16(a, dtype, gpu) for a in (q, k, vt)] + [out, dev(tiles, gpu)]
 
     def run():
         check(lib.laya_op_attention(*[p(a) for a in args], m, h, max_tiles, mode, waves, DTYPES[dtype][0], stream()))
