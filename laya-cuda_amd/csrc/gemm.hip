@@ -120,6 +120,17 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int lrow = lane & 31, kg = lane >> 5;
+  // Small wave tiles fetch their bias at kernel start (16 floats per 32 columns per lane), so its
+  // latency hides under the main loop instead of opening the epilogue.
+  constexpr bool kEarlyBias = TN == 1;
+  const bool with_bias = (E != Epi::F32 || a.splits == 1) && a.bias;
+  float4 early_bias[4];
+  if constexpr (kEarlyBias) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+      early_bias[r4] = with_bias ? *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + 8 * r4 + 4 * kg)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   auto compute = [&](int buf) {
     const T* cA = sA + buf * BM * BK;
     const T* cB = sB + buf * BN * BK;
@@ -187,8 +198,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
       for (int r4 = 0; r4 < 4; ++r4) {
         const int col = n0 + wn0 + j * 32 + 8 * r4 + 4 * kg;
         float v[4] = {acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2], acc[i][j][4 * r4 + 3]};
-        if ((E != Epi::F32 || a.splits == 1) && a.bias) {
-          const float4 b = *reinterpret_cast<const float4*>(a.bias + col);
+        if (with_bias) {
+          const float4 b = kEarlyBias ? early_bias[r4] : *reinterpret_cast<const float4*>(a.bias + col);
           v[0] = v[0] + b.x; v[1] = v[1] + b.y; v[2] = v[2] + b.z; v[3] = v[3] + b.w;
         }
         if constexpr (E == Epi::F32) {

@@ -24,6 +24,8 @@ __global__ __launch_bounds__(256) void head_gather_kernel(HeadGatherArgs a) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= a.cap || r >= *a.n_sel) return;
+  NormParams<D> np;
+  np.load(a.gamma, a.beta, lane);
   const int src = a.sel_src[r];
   float v[D / 64];
   load_row<D>(a.residual + static_cast<size_t>(src) * D, lane, v);
@@ -34,7 +36,7 @@ __global__ __launch_bounds__(256) void head_gather_kernel(HeadGatherArgs a) {
     for (int i = 0; i < D / 64; ++i) v[i] = v[i] + t[i];
   }
   store_row<D>(a.selected + static_cast<size_t>(r) * D, lane, v);
-  normalize<D>(v, lane, a.gamma, a.beta, a.eps);
+  normalize<D>(v, np, a.eps);
   store_row<D>(a.normed + static_cast<size_t>(r) * D, lane, v);
 }
 

@@ -16,6 +16,8 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(EmbedArgs a) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
+  NormParams<D> np;
+  if (a.gamma) np.load(a.gamma, a.beta, lane);
   int id = a.ids[row];
   id = id < 0 ? 0 : (id >= a.vocab ? a.vocab - 1 : id);  // host validates; never read out of bounds
   float v[D / 64];
@@ -34,7 +36,7 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(EmbedArgs a) {
 #pragma unroll
     for (int i = 0; i < D / 64; ++i) v[i] = v[i] + t[i];
   }
-  if (a.gamma) normalize<D>(v, lane, a.gamma, a.beta, a.eps);
+  if (a.gamma) normalize<D>(v, np, a.eps);
   if (a.out32) store_row<D>(a.out32 + static_cast<size_t>(row) * D, lane, v);
   if (a.out16) store_row16<D, T>(static_cast<T*>(a.out16) + static_cast<size_t>(row) * D, lane, v);
 }
@@ -45,6 +47,8 @@ __global__ __launch_bounds__(256) void add_norm_kernel(AddNormArgs a) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
   const size_t off = static_cast<size_t>(row) * D;
+  NormParams<D> np;
+  if (a.gamma) np.load(a.gamma, a.beta, lane);
   float v[D / 64];
   load_row<D>(a.residual + off, lane, v);
   if (a.parts) {
@@ -68,7 +72,7 @@ __global__ __launch_bounds__(256) void add_norm_kernel(AddNormArgs a) {
     for (int i = 0; i < D / 64; ++i) v[i] = v[i] + br[i];
   }
   if (a.sum_out) store_row<D>(a.sum_out + off, lane, v);
-  if (a.gamma) normalize<D>(v, lane, a.gamma, a.beta, a.eps);
+  if (a.gamma) normalize<D>(v, np, a.eps);
   if (a.out32) store_row<D>(a.out32 + off, lane, v);
   if (a.out16) store_row16<D, T>(static_cast<T*>(a.out16) + off, lane, v);
 }

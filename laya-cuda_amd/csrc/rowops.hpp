@@ -62,11 +62,25 @@ __device__ __forceinline__ void store_row16(T* dst, int lane, const float (&v)[D
   }
 }
 
+// LayerNorm parameters of a row, loaded into registers at kernel start so that their latency
+// overlaps the row's own loads instead of following the reductions.
+template <int D> struct NormParams {
+  float g[D / 64], b[D / 64];
+  __device__ __forceinline__ void load(const float* gamma, const float* beta, int lane) {
+    if (gamma) load_row<D>(gamma, lane, g);
+    if (beta) {
+      load_row<D>(beta, lane, b);
+    } else {
+#pragma unroll
+      for (int i = 0; i < D / 64; ++i) b[i] = 0.f;
+    }
+  }
+};
+
 // In-register LayerNorm of one row: two passes (mean, then centred variance) as in
 // laya_cuda/kernels.cu:38-46, with wave butterflies for the sums.
 template <int D>
-__device__ __forceinline__ void normalize(float (&v)[D / 64], int lane, const float* gamma, const float* beta,
-                                          float eps) {
+__device__ __forceinline__ void normalize(float (&v)[D / 64], const NormParams<D>& p, float eps) {
   constexpr int N = D / 64;
   float s = 0.f;
 #pragma unroll
@@ -79,16 +93,8 @@ __device__ __forceinline__ void normalize(float (&v)[D / 64], int lane, const fl
     sq += c * c;
   }
   const float inv = 1.0f / sqrtf(wave_sum(sq) / static_cast<float>(D) + eps);
-  float g[N], b[N];
-  load_row<D>(gamma, lane, g);
-  if (beta) {
-    load_row<D>(beta, lane, b);
-  } else {
 #pragma unroll
-    for (int i = 0; i < N; ++i) b[i] = 0.f;
-  }
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = (v[i] - mean) * inv * g[i] + b[i];
+  for (int i = 0; i < N; ++i) v[i] = (v[i] - mean) * inv * p.g[i] + p.b[i];
 }
 
 }  // namespace laya
