@@ -20,7 +20,8 @@ Fields:
                         events over back-to-back launches on the engine's stream
   cpu_baseline          the NumPy FP32 restatement of the same forward on this host's cores
   parity                GPU logits vs that CPU forward: max |logit error|, decisions equal
-``--eager`` launches the forward kernel by kernel instead of replaying its hipGraph (for
+``--calibrate-copy`` first runs a 64 MiB device copy (the reference for the HBM byte counters of a
+``rocprofv3 --pmc`` run).  ``--eager`` launches the forward kernel by kernel instead of replaying its hipGraph (for
 profilers that cannot follow graph launches).  ``--extras`` adds the other workloads: 83- and 1,024-token latency, the 32-request ragged batch
 (sequences/s) and the 24-layer d=1024 64 x 1024 batch (sequences/s and MFMA utilisation).
 """
@@ -137,9 +138,39 @@ def cpu_baseline(spec, weights, sequences, questions, seconds):
     return times, threads, out
 
 
+TRAFFIC = ROOT / "profiles" / "traffic.json"
+
+
+def measured_traffic(stage):
+    """HBM bytes per launch of ``stage`` at the 512-token workload, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (profiles/traffic.json, copy-kernel calibrated), if they cover it."""
+    try:
+        data = json.loads(TRAFFIC.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = data.get("stages", {}).get(stage)
+    return None if entry is None else entry.get("bytes_per_launch")
+
+
+def calibrate_copy():
+    """A plain device-to-device copy of 64 MiB, three times: the known-size reference that scales
+    the FETCH_SIZE and WRITE_SIZE counters of the same profiler run."""
+    import torch
+    src = torch.ones(16 << 20, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def run_headline(args):
     from laya_cuda import synthetic
     from laya_cuda.runtime import Runtime
+
+    if args.calibrate_copy:
+        calibrate_copy()
+        progress("copy calibration done")
 
     spec = synthetic.adapter("l512", mfma_dtype="float16")
     weights = synthetic.weights(spec, seed=0)
@@ -167,7 +198,7 @@ def run_headline(args):
         "predict_p50_ms": round(pct(r["api"], 50), 4), "predict_p95_ms": round(pct(r["api"], 95), 4),
         "first_ms": round(r["first_ms"], 3), "graph_replay": not args.eager,
         "tflops_forward": round(synthetic.valid_flops(spec, [512]) / (pct(r["gpu"], 50) * 1e-3) / 1e12, 2),
-        "roofline": roofline(dominant),
+        "roofline": dict(roofline(dominant), traffic=measured_traffic(dominant["stage"])),
         "stages_us_per_forward": {row["stage"]: round(row["forward_ms"] * 1e3, 2) for row in rows},
     }
     if args.cpu_seconds > 0:
@@ -239,6 +270,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--extras", action="store_true")
     ap.add_argument("--eager", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the encoder path shards by request with no collective, and "

@@ -66,6 +66,22 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], fl
     for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
 }
 
+// Workgroup -> (tile, head).  Workgroups are dealt to the 8 XCDs round-robin by linear id; when the
+// count allows, each XCD instead gets a contiguous, head-major share, so all query tiles of a
+// (sequence, head) pair run on one XCD and its K and V are fetched into that L2 once.
+__device__ __forceinline__ void work_item(int nx, int ny, int* tile, int* head) {
+  const int total = nx * ny;
+  if (total % 8) {
+    *tile = blockIdx.x;
+    *head = blockIdx.y;
+    return;
+  }
+  const int id = blockIdx.x + nx * blockIdx.y;
+  const int l = (id % 8) * (total / 8) + id / 8;
+  *head = l / nx;
+  *tile = l - *head * nx;
+}
+
 // One 64-key block of K and V^T moved from HBM to LDS by NTH cooperating threads: global loads
 // are row-contiguous 16-byte chunks (8 lanes per 128-byte row), LDS rows are 128 bytes with the
 // chunk index XOR-swizzled by (row & 7).  V^T rows store keys permuted within each 16-key group
@@ -173,8 +189,8 @@ __device__ __forceinline__ void attention_shared(const AttnArgs& a) {
   typedef typename Vec4<T>::type T4;
   constexpr int NT = 64 * NW;
 
-  const int tile = blockIdx.x, head = blockIdx.y;
-  if (tile >= a.max_tiles) return;
+  int tile, head;
+  work_item(a.max_tiles, a.heads, &tile, &head);
   const int4 td = reinterpret_cast<const int4*>(a.tiles)[tile];
   const int row0 = td.x, row1 = td.y, start = td.z, len = td.w;
   if (row0 >= row1) return;
@@ -258,8 +274,8 @@ __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
   constexpr int OP = 65;  // LDS pitch of a merged query row (floats): conflict-free column writes
   constexpr int STAGE = 2 * 2 * KB * 64;  // per wave: two buffers of K and V^T (16-bit elements)
 
-  const int tile = blockIdx.x, head = blockIdx.y;
-  if (tile >= a.max_tiles) return;
+  int tile, head;
+  work_item(a.max_tiles, a.heads, &tile, &head);
   const int4 td = reinterpret_cast<const int4*>(a.tiles)[tile];
   const int row0 = td.x, row1 = td.y, start = td.z, len = td.w;
   if (row0 >= row1) return;

@@ -28,30 +28,33 @@ namespace {
 
 constexpr int BK = 64;
 
-// Workgroup tile coordinates.  Workgroups are dealt to the 8 XCDs round-robin by linear id, so
-// consecutive ids run on different L2s.  When the tile count allows, each XCD instead gets a
-// contiguous share of the tile space, walked in groups of 4 tile rows (columns), column (row)
-// index outer: the operand that is larger in HBM (A for many rows, B otherwise) is then fetched
-// into one XCD's L2 once and reused from there, and the group keeps the smaller operand's tile
-// resident while it is reused 4 times.
-__device__ __forceinline__ void tile_coords(int nx, int ny, bool rows_major, int* x, int* y) {
-  const int id = blockIdx.x + nx * blockIdx.y;
-  const int total = nx * ny;
+// Workgroup tile coordinates.  Workgroups are dealt to the 8 XCDs round-robin by linear dispatch
+// id, so consecutive ids run on different L2s.  When the workgroup count allows, the logical index
+// is laid out instead so that each XCD gets one contiguous share, decoded split-major: with split-K
+// an XCD works on whole K-slices (or an equal part of one) and fetches only those slices of both
+// operands.  Inside a slice, tiles are walked so the operand that is larger in HBM is fetched into
+// one L2 once: with many rows (A larger), groups of 4 tile rows with the column index outer; with
+// fewer rows than columns (B, the weights, larger), whole tile columns one after another.
+__device__ __forceinline__ void tile_coords(int nx, int ny, int nz, bool rows_major, int* x, int* y, int* z) {
+  const int per_z = nx * ny, total = per_z * nz;
   if (total % 8) {
     *x = blockIdx.x;
     *y = blockIdx.y;
+    *z = blockIdx.z;
     return;
   }
-  const int t = (id % 8) * (total / 8) + id / 8;
-  constexpr int G = 4;
+  const int id = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
+  const int l = (id % 8) * (total / 8) + id / 8;
+  *z = l / per_z;
+  const int t = l - *z * per_z;
   if (rows_major) {
+    constexpr int G = 4;
     const int group = t / (G * nx), first = group * G, size = min(G, ny - first), in = t - group * G * nx;
     *y = first + in % size;
     *x = in / size;
   } else {
-    const int group = t / (G * ny), first = group * G, size = min(G, nx - first), in = t - group * G * ny;
-    *x = first + in % size;
-    *y = in / size;
+    *x = t / ny;
+    *y = t - *x * ny;
   }
 }
 
@@ -74,9 +77,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
-  int tx, ty;
-  tile_coords(gridDim.x, gridDim.y, a.rows_major, &tx, &ty);
-  const int n0 = tx * BN, m0 = ty * BM, z = blockIdx.z;
+  int tx, ty, z;
+  tile_coords(gridDim.x, gridDim.y, gridDim.z, a.rows_major, &tx, &ty, &z);
+  const int n0 = tx * BN, m0 = ty * BM;
 
   const T* A = static_cast<const T*>(a.a);
   const T* B = static_cast<const T*>(a.b);

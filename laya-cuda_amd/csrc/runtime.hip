@@ -9,6 +9,7 @@
 //     packed inputs are uploaded with one H2D copy before the launch (runtime.py:52-68, 115-133).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <list>
@@ -141,7 +142,7 @@ struct Slot {
   float *selected = nullptr, *normed = nullptr, *hpart = nullptr, *logits = nullptr, *acts = nullptr;
   float *row_logit = nullptr, *feat = nullptr, *apart = nullptr;
   int tile[4] = {0, 0, 0, 0}, splits[4] = {1, 1, 1, 1};  // qkv, o, up, down
-  int attn_mode = 0, attn_waves = 2, head_splits = 1, act_splits = 1;
+  int attn_mode = 0, attn_waves = 2, attn_tiles = 0, head_splits = 1, act_splits = 1;
   hipGraphExec_t graph = nullptr;
   hipEvent_t start = nullptr, end = nullptr;
 };
@@ -273,6 +274,10 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
       s->attn_mode = kAttnSplitKeys;
       s->attn_waves = 2;
     }
+    // Tiles of at most `block` rows: every sequence, and every run of rows between or after
+    // sequences, adds at most one partial tile, so this bounds the work list of any request.
+    const int block = attention_block_rows(s->attn_mode, s->attn_waves);
+    s->attn_tiles = std::min(s->L.T, m / block + 2 * b + 1);
     s->head_splits = head_gemm_splits(s->L.R, d, d, E.cus);
     s->act_splits = head_gemm_splits(b, c.act_hidden, E.act_k, E.cus);
     const int max_split = s->splits[1] > s->splits[3] ? s->splits[1] : s->splits[3];
@@ -344,7 +349,7 @@ void derive_inputs(const Engine& E, Slot& s) {
                  "sequences must start at increasing multiples of 16 rows and fit the shape class");
   }
   const int nt = build_attention_tiles(P + L.starts, P + L.lengths, n_seq, m,
-                                       attention_block_rows(s.attn_mode, s.attn_waves), P + L.tiles, L.T);
+                                       attention_block_rows(s.attn_mode, s.attn_waves), P + L.tiles, s.attn_tiles);
   LAYA_REQUIRE(nt >= 0, "attention tile list overflow");
   // Compact head rows: per question its CLS row then its option rows.
   int ns = 0;
@@ -403,7 +408,7 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       check_launch(launch_gemm(g, Epi::QKV, t, s.tile[0], st), "qkv");
       break;
     case kAttention: {
-      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, m, c.heads, L.T};
+      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, m, c.heads, s.attn_tiles};
       check_launch(launch_attention(aa, t, s.attn_mode, s.attn_waves, st), "attention");
       break;
     }
