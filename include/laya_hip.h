@@ -62,6 +62,8 @@ typedef struct LayaConfig {
   int32_t act_hidden;     /* act-head hidden width (256 in Laya) */
   int32_t max_len;        /* longest sequence, tokens */
   int32_t mfma_dtype;     /* LAYA_BF16 or LAYA_F16: resident matrices and MFMA operands */
+  float theta_global;     /* RoPE theta of global layers (LAYA_POS_ROPE; laya.py:72-78) */
+  float theta_local;      /* RoPE theta of local (windowed) layers */
 } LayaConfig;
 
 /* Shape class of one predict: the reference's slot key (laya_cuda/runtime.py:20-25). */
@@ -166,22 +168,30 @@ int laya_op_norm(float* residual, const float* branch, int splits, int64_t part_
                  float* sum_out, float* out32, void* out16, int dtype16, int rows, int width,
                  void* stream);
 
-/* Ops.linear (ops.py:58-66): out[M][N] = x[M][K] w[N][K]^T (+ bias).  kind 0: fp32 out
- * (split-K partials at out + z*M*N when splits > 1, bias then must be NULL), 1: 16-bit out,
- * 2: 16-bit GELU out.  tile < 0 lets the planner choose tile and splits (splits ignored). */
+/* Ops.linear (ops.py:58-66) with the activate modes (kernels.cu:59-67) as epilogues:
+ * out[M][N] = x[M][K] w[N][K]^T (+ bias).  kind 0: fp32 out (split-K partials at out + z*M*N when
+ * splits > 1, bias then must be NULL), 1: 16-bit out, 2: 16-bit exact-GELU out, 3: 16-bit ReLU out,
+ * 4: GeGLU, out[M][N/2] = gelu(gate) * value with w's rows in the resident GeGLU interleave
+ * (32-row groups: 16 gate rows, then their 16 value rows).  tile < 0 lets the planner choose tile
+ * and splits (splits ignored). */
 int laya_op_linear(const void* x, const void* w, const float* bias, void* out, int kind,
                    int dtype16, int M, int N, int K, int splits, int tile, void* stream);
 
 /* QKV projection with the head-major epilogue that replaces `layout` (kernels.cu:68-82):
- * q, k [heads][M][64], vt [heads][64][M]. */
+ * q, k [heads][M][64], vt [heads][64][M].  With rope_cos non-NULL, Q and K are rotated (rotate-half
+ * RoPE, kernels.cu:73-77) in fp32 before rounding, by the [positions][32] cos/sin tables at each
+ * row's positions[row]. */
 int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* k, void* vt,
-                int dtype16, int M, int width, int tile, void* stream);
+                const float* rope_cos, const float* rope_sin, const int32_t* positions, int dtype16,
+                int M, int width, int tile, void* stream);
 
-/* attention (kernels.cu:90-154, window -1) over a device copy (16-byte aligned) of a tile list from
+/* attention (kernels.cu:90-154) over a device copy (16-byte aligned) of a tile list from
  * laya_attention_tiles built with laya_attention_block(mode, waves) rows per tile; q, k [heads][m][64],
- * vt [heads][64][m], out [m][heads*64]. */
+ * vt [heads][64][m], out [m][heads*64]; window >= 0 keeps only keys with |query - key| <= window (the
+ * local layers, kernels.cu:106-107), window < 0 is global attention. */
 int laya_op_attention(const void* q, const void* k, const void* vt, void* out, const int32_t* tiles,
-                      int m, int heads, int max_tiles, int mode, int waves, int dtype16, void* stream);
+                      int m, int heads, int max_tiles, int mode, int waves, int window, int dtype16,
+                      void* stream);
 
 #ifdef __cplusplus
 }

@@ -25,20 +25,26 @@ namespace {
 
 constexpr int KB = 64;  // keys per block
 
-// One 64-key block of the single-pass softmax for this lane's query.  s holds the raw QK^T
+// One 64-key block of the single-pass softmax for this lane's query q.  s holds the raw QK^T
 // scores of keys kb + 32kt + 8(r/4) + 4g + r%4 (the S^T accumulator layout); the running max
 // `mrow` is kept in the scaled log2 domain (x * log2(e) / 8), so each probability costs one FMA
-// and one exp2.  Keys at or past kend are masked only in the block that contains kend.  On
-// return s holds the block's unnormalised probabilities, lsum and o are rescaled.
+// and one exp2.  Keys outside this lane's visible range [qlo, qhi) are masked: the sequence's end,
+// and on local layers the keys farther than the window from the query (kernels.cu:106-107).  Only
+// blocks flagged `edge` by the caller can hold such keys.  The mask is a select per score, not a
+// branch.  A block whose keys are all masked for this query leaves its state untouched.  On return
+// s holds the block's unnormalised probabilities, lsum and o are rescaled.
 __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], float& mrow, float& lsum, int kb,
-                                              int kend, int g) {
+                                              bool edge, int qlo, int qhi, int g) {
   constexpr float c = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) in the exp2 domain
-  if (kb + KB > kend) {
+  if (edge) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (kb + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= kend) s[kt][r] = -INFINITY;
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        const bool out = (key < qlo) | (key >= qhi);
+        s[kt][r] = out ? -INFINITY : s[kt][r];
+      }
   }
   float mx[4] = {s[0][0], s[0][1], s[0][2], s[0][3]};
 #pragma unroll
@@ -48,14 +54,15 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], fl
   float bmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
   bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
   const float mnew = fmaxf(mrow, bmax * c);
-  const float alpha = __builtin_amdgcn_exp2f(mrow - mnew);  // first block: exp2(-inf) = 0
+  const float base = mnew == -INFINITY ? 0.f : mnew;      // nothing seen yet: probabilities are 0
+  const float alpha = __builtin_amdgcn_exp2f(mrow - base);  // first block: exp2(-inf) = 0
   mrow = mnew;
   float part[4] = {0.f, 0.f, 0.f, 0.f};  // four independent sums: a short dependency chain
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], c, -mnew));  // masked: exp2(-inf) = 0
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], c, -base));  // masked: exp2(-inf) = 0
       s[kt][r] = p;
       part[r & 3] += p;
     }
@@ -125,7 +132,8 @@ struct KVStage {
 // 16 keys), the online-softmax step, and O^T += V^T P^T with P straight from registers.
 template <typename T>
 __device__ __forceinline__ void attend_block(const T* sK, const T* sV, const typename Vec8<T>::type (&qf)[4],
-                                             f32x16 (&o)[2], float& mrow, float& lsum, int kb, int kend, int lane) {
+                                             f32x16 (&o)[2], float& mrow, float& lsum, int kb, bool edge, int qlo,
+                                             int qhi, int lane) {
   typedef typename Vec8<T>::type T8;
   const int ql = lane & 31, g = lane >> 5;
   f32x16 s[2];
@@ -141,7 +149,7 @@ __device__ __forceinline__ void attend_block(const T* sK, const T* sV, const typ
       s[kt] = mfma32(kf, qf[ks], s[kt]);
     }
   }
-  softmax_block(s, o, mrow, lsum, kb, kend, g);
+  softmax_block(s, o, mrow, lsum, kb, edge, qlo, qhi, g);
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     T8 pb;
@@ -224,14 +232,21 @@ __device__ __forceinline__ void attention_shared(const AttnArgs& a) {
     for (int r = 0; r < 16; ++r) o[d][r] = 0.f;
   float mrow = -INFINITY, lsum = 0.f;
 
-  const int nkb = (len + KB - 1) / KB;
-  st.load(K, Vt, a.m, start, tid);
+  // Keys this tile can see: the whole sequence, or on local layers the window around its rows
+  // (first block 16-aligned, so the 16-byte V^T loads stay aligned); this lane's query sees [qlo, qhi).
+  const bool local = a.window >= 0;
+  const int klo = local ? max(start, (row0 - a.window) & ~15) : start;
+  const int khi = local ? min(kend, row1 + a.window) : kend;
+  const int nkb = (khi - klo + KB - 1) / KB;
+  const int qlo = local ? max(start, q - a.window) : start;
+  const int qhi = local ? max(qlo, min(kend, q + a.window + 1)) : kend;
+  st.load(K, Vt, a.m, klo, tid);
   st.store(sK[0], sV[0], tid);
   __syncthreads();
   for (int j = 0; j < nkb; ++j) {
-    const int cur = j & 1, kb = start + j * KB;
+    const int cur = j & 1, kb = klo + j * KB;
     if (j + 1 < nkb) st.load(K, Vt, a.m, kb + KB, tid);
-    attend_block<T>(sK[cur], sV[cur], qf, o, mrow, lsum, kb, kend, lane);
+    attend_block<T>(sK[cur], sV[cur], qf, o, mrow, lsum, kb, local || kb + KB > kend, qlo, qhi, lane);
     if (j + 1 < nkb) st.store(sK[cur ^ 1], sV[cur ^ 1], tid);
     __syncthreads();
   }
@@ -312,14 +327,20 @@ __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
   float mrow = -INFINITY, lsum = 0.f;
 
   // LDS accesses of one wave execute in issue order, so a wave's own staging needs no barrier.
-  const int nkb = (len + KB - 1) / KB;
-  if (wave < nkb) st.load(K, Vt, a.m, start + KB * wave, lane);
+  // Key range of the tile and of this lane's query as in attention_shared.
+  const bool local = a.window >= 0;
+  const int klo = local ? max(start, (row0 - a.window) & ~15) : start;
+  const int khi = local ? min(kend, row1 + a.window) : kend;
+  const int nkb = (khi - klo + KB - 1) / KB;
+  const int qlo = local ? max(start, q - a.window) : start;
+  const int qhi = local ? max(qlo, min(kend, q + a.window + 1)) : kend;
+  if (wave < nkb) st.load(K, Vt, a.m, klo + KB * wave, lane);
   for (int j = wave, it = 0; j < nkb; j += NW, ++it) {
     T* sK = mine + (it & 1) * 2 * KB * 64;
     T* sV = sK + KB * 64;
     st.store(sK, sV, lane);
-    if (j + NW < nkb) st.load(K, Vt, a.m, start + KB * (j + NW), lane);
-    attend_block<T>(sK, sV, qf, o, mrow, lsum, start + KB * j, kend, lane);
+    if (j + NW < nkb) st.load(K, Vt, a.m, klo + KB * (j + NW), lane);
+    attend_block<T>(sK, sV, qf, o, mrow, lsum, klo + KB * j, local || klo + KB * (j + 1) > kend, qlo, qhi, lane);
   }
 
   // Merge the waves' partial results: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w.

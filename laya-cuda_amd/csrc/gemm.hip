@@ -190,42 +190,116 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
   }
 
   // Epilogue.  Element r of lane l in a 32x32 tile of C^T is output column 8*(r/4) + 4*(l/32) +
-  // r%4 of output row l%32: a lane holds columns c..c+3 of one row for each r/4.
+  // r%4 of output row l%32: a lane holds columns c..c+3 of one row for each r/4.  The bias joins in
+  // fp32 before the single rounding.
+  auto take = [&](int i, int j, int r4, float (&v)[4]) {
+    v[0] = acc[i][j][4 * r4];
+    v[1] = acc[i][j][4 * r4 + 1];
+    v[2] = acc[i][j][4 * r4 + 2];
+    v[3] = acc[i][j][4 * r4 + 3];
+    if (with_bias) {
+      const float4 b = kEarlyBias ? early_bias[r4]
+                                  : *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + j * 32 + 8 * r4 + 4 * kg);
+      v[0] = v[0] + b.x; v[1] = v[1] + b.y; v[2] = v[2] + b.z; v[3] = v[3] + b.w;
+    }
+  };
+  typedef typename Vec4<T>::type T4;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int row = m0 + wm0 + i * 32 + lrow;
     if (row >= a.M) continue;
+    if constexpr (E == Epi::QKV) {
+      if (a.rope_cos) {
+        // RoPE on Q and K (rotate-half, the reference's `layout`, kernels.cu:73-77) on the fp32
+        // accumulator before the single rounding: tiles j and j+1 hold dims d and d+32 of one head.
+        const int pos = a.positions[row];
+        const float* cs = a.rope_cos + static_cast<size_t>(pos) * 32;
+        const float* sn = a.rope_sin + static_cast<size_t>(pos) * 32;
+#pragma unroll
+        for (int j = 0; j + 1 < TN; j += 2) {
+          const int col = n0 + wn0 + j * 32;
+          const int part = col / a.width, hn = col - part * a.width, head = hn >> 6;
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int dim = 8 * r4 + 4 * kg;
+            T4 lo, hi;
+            float v0[4], v1[4];
+            take(i, j, r4, v0);
+            take(i, j + 1, r4, v1);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float x0 = v0[e], x1 = v1[e];
+              if (part < 2) {
+                const float c = cs[dim + e], sv = sn[dim + e];
+                const float y0 = x0 * c - x1 * sv, y1 = x1 * c + x0 * sv;
+                x0 = y0;
+                x1 = y1;
+              }
+              lo[e] = to_half<T>(x0);
+              hi[e] = to_half<T>(x1);
+            }
+            if (part < 2) {
+              T* dst = static_cast<T*>(part == 0 ? a.q : a.k) + (static_cast<size_t>(head) * a.M + row) * 64 + dim;
+              *reinterpret_cast<T4*>(dst) = lo;
+              *reinterpret_cast<T4*>(dst + 32) = hi;
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                static_cast<T*>(a.vt)[(static_cast<size_t>(head) * 64 + dim + e) * a.M + row] = lo[e];
+                static_cast<T*>(a.vt)[(static_cast<size_t>(head) * 64 + 32 + dim + e) * a.M + row] = hi[e];
+              }
+            }
+          }
+        }
+        continue;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
+      if constexpr (E == Epi::GEGLU) {
+        // Weight rows interleaved in 32-row groups (16 gate rows, then their 16 value rows), so a
+        // lane holds gate column c (r4 < 2) and its value column c + 16 (r4 + 2):
+        // out[f] = gelu(gate) * value, 16 features per 32 columns (the reference's activate mode 2).
+        const int fbase = ((n0 + wn0 + j * 32) >> 1) + 4 * kg;
+#pragma unroll
+        for (int r4 = 0; r4 < 2; ++r4) {
+          float gate[4], value[4];
+          take(i, j, r4, gate);
+          take(i, j, r4 + 2, value);
+          T4 h;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = to_half<T>(gelu16(gate[e]) * value[e]);
+          *reinterpret_cast<T4*>(static_cast<T*>(a.out) + static_cast<long long>(row) * a.ldo + fbase + 8 * r4) = h;
+        }
+        continue;
+      }
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         const int col = n0 + wn0 + j * 32 + 8 * r4 + 4 * kg;
-        float v[4] = {acc[i][j][4 * r4], acc[i][j][4 * r4 + 1], acc[i][j][4 * r4 + 2], acc[i][j][4 * r4 + 3]};
-        if (with_bias) {
-          const float4 b = kEarlyBias ? early_bias[r4] : *reinterpret_cast<const float4*>(a.bias + col);
-          v[0] = v[0] + b.x; v[1] = v[1] + b.y; v[2] = v[2] + b.z; v[3] = v[3] + b.w;
-        }
+        float v[4];
+        take(i, j, r4, v);
         if constexpr (E == Epi::F32) {
           *reinterpret_cast<float4*>(static_cast<float*>(a.out) + z * a.split_stride +
                                      static_cast<long long>(row) * a.ldo + col) = make_float4(v[0], v[1], v[2], v[3]);
         } else if constexpr (E == Epi::QKV) {
           const int part = col / a.width, hn = col - part * a.width, head = hn >> 6, dim = hn & 63;
-          typename Vec4<T>::type h;
+          T4 h;
 #pragma unroll
           for (int e = 0; e < 4; ++e) h[e] = to_half<T>(v[e]);
           if (part < 2) {
             T* dst = static_cast<T*>(part == 0 ? a.q : a.k);
-            *reinterpret_cast<typename Vec4<T>::type*>(dst + (static_cast<size_t>(head) * a.M + row) * 64 + dim) = h;
+            *reinterpret_cast<T4*>(dst + (static_cast<size_t>(head) * a.M + row) * 64 + dim) = h;
           } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               static_cast<T*>(a.vt)[(static_cast<size_t>(head) * 64 + dim + e) * a.M + row] = h[e];
           }
         } else {
-          typename Vec4<T>::type h;
+          T4 h;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = to_half<T>(E == Epi::GELU ? gelu16(v[e]) : v[e]);
-          *reinterpret_cast<typename Vec4<T>::type*>(static_cast<T*>(a.out) + static_cast<long long>(row) * a.ldo + col) = h;
+          for (int e = 0; e < 4; ++e)
+            h[e] = to_half<T>(E == Epi::GELU ? gelu16(v[e]) : E == Epi::RELU ? fmaxf(v[e], 0.f) : v[e]);
+          *reinterpret_cast<T4*>(static_cast<T*>(a.out) + static_cast<long long>(row) * a.ldo + col) = h;
         }
       }
     }
@@ -303,6 +377,8 @@ hipError_t set_lds_all() {
   if (e == hipSuccess) e = set_lds_attr<T, Epi::HALF>();
   if (e == hipSuccess) e = set_lds_attr<T, Epi::GELU>();
   if (e == hipSuccess) e = set_lds_attr<T, Epi::QKV>();
+  if (e == hipSuccess) e = set_lds_attr<T, Epi::RELU>();
+  if (e == hipSuccess) e = set_lds_attr<T, Epi::GEGLU>();
   return e;
 }
 
@@ -317,16 +393,17 @@ hipError_t gemm_prepare() {
   return e;
 }
 
-void gemm_plan(int M, int N, int K, Epi epi, int cus, int* tile, int* splits) {
+void gemm_plan(int M, int N, int K, Epi epi, int cus, int* tile, int* splits, bool rope) {
   // Largest tile that still gives every CU a workgroup; small problems fall back to small tiles
   // and, for the fp32 (split-K capable) epilogue, to K splits until the grid covers the chip.
   // Eight-wave tiles first: with two waves per SIMD they sustain the most MFMA throughput when
   // the grid is large enough; then four-wave tiles from large to small.
   const int order[] = {7, 9, 8, 0, 1, 2, 3, 4, 5, 6};
-  int best = 5, best_split = 1;
+  int best = rope ? 4 : 5, best_split = 1;
   for (int id : order) {
     const TileDef& d = kTiles[id];
     if (N % d.bn) continue;
+    if (rope && (d.bn / d.wn) % 64) continue;
     const long long wgs = static_cast<long long>((M + d.bm - 1) / d.bm) * (N / d.bn);
     const long long waste_rows = static_cast<long long>((M + d.bm - 1) / d.bm) * d.bm - M;
     if (waste_rows * 4 > M) continue;  // more than 25% padding rows
@@ -354,6 +431,10 @@ hipError_t launch_gemm(const GemmArgs& args, Epi epi, DType t, int tile, hipStre
   if (a.M <= 0) return hipSuccess;
   if (a.K % BK || a.N % kTiles[tile].bn || a.splits < 1) return hipErrorInvalidValue;
   if (epi != Epi::F32 && a.splits != 1) return hipErrorInvalidValue;
+  // RoPE needs both halves of a head in one lane: wave tiles of 64-column multiples.
+  const TileDef& td = kTiles[tile];
+  if (epi == Epi::QKV && a.rope_cos && (td.bn / td.wn) % 64) return hipErrorInvalidValue;
+  if (epi == Epi::GEGLU && (a.N % 32 || a.ldo * 2 < a.N)) return hipErrorInvalidValue;
   if (epi == Epi::F32 && a.splits != 1 && a.bias) return hipErrorInvalidValue;  // bias joins the sum later
   const bool h = t == DType::F16;
   switch (epi) {
@@ -361,6 +442,8 @@ hipError_t launch_gemm(const GemmArgs& args, Epi epi, DType t, int tile, hipStre
     case Epi::HALF: return h ? launch_t<f16, Epi::HALF>(a, tile, stream) : launch_t<bf16, Epi::HALF>(a, tile, stream);
     case Epi::GELU: return h ? launch_t<f16, Epi::GELU>(a, tile, stream) : launch_t<bf16, Epi::GELU>(a, tile, stream);
     case Epi::QKV: return h ? launch_t<f16, Epi::QKV>(a, tile, stream) : launch_t<bf16, Epi::QKV>(a, tile, stream);
+    case Epi::RELU: return h ? launch_t<f16, Epi::RELU>(a, tile, stream) : launch_t<bf16, Epi::RELU>(a, tile, stream);
+    case Epi::GEGLU: return h ? launch_t<f16, Epi::GEGLU>(a, tile, stream) : launch_t<bf16, Epi::GEGLU>(a, tile, stream);
   }
   return hipErrorInvalidValue;
 }

@@ -40,6 +40,27 @@ __global__ __launch_bounds__(256) void head_gather_kernel(HeadGatherArgs a) {
   store_row<D>(a.normed + static_cast<size_t>(r) * D, lane, v);
 }
 
+template <int D, typename T>
+__global__ __launch_bounds__(256) void gather_rows_kernel(GatherRowsArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.cap) return;
+  float v[D / 64];
+  const bool live = r < *a.n;
+  const int src = live ? a.idx[r] : 0;
+  if (live) {
+    load_row<D>(a.src32 + static_cast<size_t>(src) * D, lane, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) v[i] = 0.f;
+  }
+  store_row<D>(a.dst32 + static_cast<size_t>(r) * D, lane, v);
+  // 16-bit rows: 8 elements (one 16-byte chunk) per lane per step.
+  const i32x4* s16 = reinterpret_cast<const i32x4*>(static_cast<const T*>(a.src16) + static_cast<size_t>(src) * D);
+  i32x4* d16 = reinterpret_cast<i32x4*>(static_cast<T*>(a.dst16) + static_cast<size_t>(r) * D);
+  for (int c = lane; c < D / 8; c += 64) d16[c] = live ? s16[c] : i32x4{0, 0, 0, 0};
+}
+
 // fp32 GEMM on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): parts[z] = X W^T over split z.
 // Workgroup tile 32 rows x 64 cols, 4 waves of 16x32; K staged in 32-wide LDS slabs.
 __global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
@@ -194,6 +215,24 @@ hipError_t launch_head_gather(const HeadGatherArgs& a, int width, hipStream_t st
   const dim3 grid((a.cap + 3) / 4), block(256);
   switch (width) {
 #define LAYA_CASE(D) case D: hipLaunchKernelGGL((head_gather_kernel<D>), grid, block, 0, stream, a); break;
+    LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
+    LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
+#undef LAYA_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const GatherRowsArgs& a, int width, DType t, hipStream_t stream) {
+  if (a.cap <= 0) return hipSuccess;
+  const dim3 grid((a.cap + 3) / 4), block(256);
+  const bool h = t == DType::F16;
+  switch (width) {
+#define LAYA_CASE(D)                                                                                      \
+  case D:                                                                                               \
+    if (h) hipLaunchKernelGGL((gather_rows_kernel<D, f16>), grid, block, 0, stream, a);                  \
+    else hipLaunchKernelGGL((gather_rows_kernel<D, bf16>), grid, block, 0, stream, a);                   \
+    break;
     LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
     LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
 #undef LAYA_CASE

@@ -36,6 +36,8 @@ struct AddNormArgs {
   float* out32;    // normalised (or sum, if gamma is null) fp32, may alias residual
   void* out16;     // same as 16-bit, or null
   int rows;
+  const float* row_table;    // [n][d] rows added per token (question types), or null
+  const int32_t* row_index;  // [rows] row of row_table for each token
 };
 
 bool norm_width_supported(int width);
@@ -43,7 +45,7 @@ hipError_t launch_embed(const EmbedArgs& a, int width, DType t, hipStream_t stre
 hipError_t launch_add_norm(const AddNormArgs& a, int width, DType t, hipStream_t stream);
 
 // ---- MFMA GEMM: out[M][N] = A[M][K] * B[N][K]^T (+ bias), fp32 accumulate ----
-enum class Epi : int { F32 = 0, HALF = 1, GELU = 2, QKV = 3 };
+enum class Epi : int { F32 = 0, HALF = 1, GELU = 2, QKV = 3, RELU = 4, GEGLU = 5 };
 
 struct GemmArgs {
   const void* a;  // [M][lda] 16-bit
@@ -60,6 +62,10 @@ struct GemmArgs {
   void* k;
   void* vt;
   int width;
+  // QKV with RoPE (null: none): cos/sin [positions][32] of this layer's theta, positions [M].
+  const float* rope_cos;
+  const float* rope_sin;
+  const int32_t* positions;
   int rows_major;  // XCD share of the tile grid split by tile rows (A larger than B) or columns
 };
 
@@ -69,7 +75,8 @@ struct GemmTile {
 int gemm_tile_count();
 GemmTile gemm_tile(int id);
 // Chooses a tile and split count for a problem on `cus` compute units.
-void gemm_plan(int M, int N, int K, Epi epi, int cus, int* tile, int* splits);
+// rope: the QKV epilogue applies RoPE, which needs wave tiles of 64-column multiples.
+void gemm_plan(int M, int N, int K, Epi epi, int cus, int* tile, int* splits, bool rope = false);
 hipError_t gemm_prepare();  // sets LDS attributes of the large-tile kernels (call once per device)
 hipError_t launch_gemm(const GemmArgs& a, Epi epi, DType t, int tile, hipStream_t stream);
 
@@ -85,6 +92,7 @@ struct AttnArgs {
   void* out;       // [m][heads*64]
   const int32_t* tiles;  // [max_tiles][4] = (row0, row1, kstart, klen)
   int m, heads, max_tiles;
+  int window;  // local attention half-window (|query - key| <= window), or -1 for global
 };
 // Host: tile list of packed sequences (starts multiples of 16, increasing, spans of 16) with at
 // most `block` query rows per tile; fills all max_tiles entries, returns the used count or -1.
@@ -114,6 +122,19 @@ struct HeadGatherArgs {
   int cap;
 };
 hipError_t launch_head_gather(const HeadGatherArgs& a, int width, hipStream_t stream);
+
+// Compact readout rows for the last head transformer layer: dst32[r] = src32[idx[r]] and
+// dst16[r] = src16[idx[r]] (bit-exact copies) for r < *n; rows n..cap-1 are zeroed.
+struct GatherRowsArgs {
+  const float* src32;
+  float* dst32;
+  const void* src16;
+  void* dst16;
+  const int32_t* idx;
+  const int32_t* n;
+  int cap;
+};
+hipError_t launch_gather_rows(const GatherRowsArgs& a, int width, DType t, hipStream_t stream);
 
 struct HeadGemmArgs {
   const float* x;  // [cap][K]

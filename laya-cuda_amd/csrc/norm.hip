@@ -71,6 +71,12 @@ __global__ __launch_bounds__(256) void add_norm_kernel(AddNormArgs a) {
 #pragma unroll
     for (int i = 0; i < D / 64; ++i) v[i] = v[i] + br[i];
   }
+  if (a.row_table) {  // question-type row of this token (type_add, kernels.cu:155-158)
+    float t[D / 64];
+    load_row<D>(a.row_table + static_cast<size_t>(a.row_index[row]) * D, lane, t);
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) v[i] = v[i] + t[i];
+  }
   if (a.sum_out) store_row<D>(a.sum_out + off, lane, v);
   if (a.gamma) normalize<D>(v, np, a.eps);
   if (a.out32) store_row<D>(a.out32 + off, lane, v);

@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <list>
@@ -86,12 +87,22 @@ struct DevTensor {
   std::vector<int64_t> shape;
   size_t count = 0;
   size_t bytes = 0;
+  bool geglu = false;  // rows resident in the GeGLU interleave (see geglu_row)
 };
 
 struct Expected {
   std::vector<int64_t> shape;
-  bool mfma = false;  // resident in the 16-bit MFMA operand type
+  bool mfma = false;   // resident in the 16-bit MFMA operand type
+  bool geglu = false;  // a [2f][d] gate|value matrix, resident with interleaved rows
 };
+
+// GeGLU up-projection rows [gate 0..f-1 | value 0..f-1] are stored in 32-row groups (16 gate rows,
+// then their 16 value rows) so the GEMM epilogue finds each gate column and its value column in
+// one lane.  Resident row r holds checkpoint row geglu_row(r, f).
+int64_t geglu_row(int64_t r, int64_t f) {
+  const int64_t group = r / 32, in = r % 32;
+  return in < 16 ? group * 16 + in : f + group * 16 + (in - 16);
+}
 
 // Packed input layout for shape (m, b, k): the caller's block (laya_packed_ints) followed by the
 // derived work lists the host builds before the single upload.
@@ -141,15 +152,31 @@ struct Slot {
   float* part = nullptr;
   float *selected = nullptr, *normed = nullptr, *hpart = nullptr, *logits = nullptr, *acts = nullptr;
   float *row_logit = nullptr, *feat = nullptr, *apart = nullptr;
+  // Last head transformer layer, on the compact readout rows: attention rows, normalised rows,
+  // FFN rows and split-K partials.
+  void *attn_sel = nullptr, *x_sel = nullptr, *ff_sel = nullptr;
+  float* part_sel = nullptr;
   int tile[4] = {0, 0, 0, 0}, splits[4] = {1, 1, 1, 1};  // qkv, o, up, down
+  // Head transformer layers: in_proj, out_proj, linear1, linear2 over all rows, then out_proj,
+  // linear1, linear2 over the readout rows.
+  int htile[7] = {0, 0, 0, 0, 0, 0, 0}, hsplits[7] = {1, 1, 1, 1, 1, 1, 1};
   int attn_mode = 0, attn_waves = 2, attn_tiles = 0, head_splits = 1, act_splits = 1;
   hipGraphExec_t graph = nullptr;
   hipEvent_t start = nullptr, end = nullptr;
 };
 
+// Encoder layer.  BERT-style: n1 = post-attention norm, n2 = post-FFN norm, biases everywhere.
+// ModernBERT: n1 = attn_norm (null in layer 0), n2 = mlp_norm, no biases (null), wi interleaved.
 struct Layer {
   const void *wqkv, *wo, *wi, *wo2;
   const float *bqkv, *bo, *bi, *bo2, *n1g, *n1b, *n2g, *n2b;
+  bool local;  // ModernBERT local layer: +-window attention, local RoPE theta
+};
+
+// Decision-head transformer layer (torch TransformerEncoderLayer, norm_first, ReLU, 4d).
+struct HeadLayer {
+  const void *in_w, *out_w, *l1_w, *l2_w;
+  const float *in_b, *out_b, *l1_b, *l2_b, *n1g, *n1b, *n2g, *n2b;
 };
 
 struct Engine {
@@ -161,6 +188,11 @@ struct Engine {
   size_t weight_bytes = 0, slot_bytes = 0;
   bool finalized = false;
   std::vector<Layer> layers;
+  std::vector<HeadLayer> head_layers;
+  bool modern = false;  // ModernBERT executor variant (pre-LN, RoPE, GeGLU, windows, head layers)
+  const float* final_norm = nullptr;
+  float* rope = nullptr;  // cos and sin tables [2 thetas][2][rope_rows][32]
+  int rope_rows = 0;
   const float *tok = nullptr, *pos = nullptr, *type0 = nullptr, *emb_g = nullptr, *emb_b = nullptr;
   const float *type_emb = nullptr, *s0w = nullptr, *s0b = nullptr, *s1w = nullptr, *s1b = nullptr;
   const float *s3w = nullptr, *s3b = nullptr, *a0w = nullptr, *a0b = nullptr, *a2w = nullptr, *a2b = nullptr;
@@ -176,8 +208,8 @@ void check_config(const LayaConfig& c) {
   LAYA_REQUIRE(c.heads > 0 && c.width == c.heads * 64, "width must equal heads * 64 (64-wide attention heads)");
   LAYA_REQUIRE(norm_width_supported(c.width), "unsupported width " + std::to_string(c.width));
   LAYA_REQUIRE(c.width % 64 == 0 && c.width >= 64, "width must be a multiple of 64");
-  LAYA_REQUIRE(c.layers >= 1 && c.intermediate > 0 && c.intermediate % 256 == 0,
-               "intermediate size must be a positive multiple of 256");
+  LAYA_REQUIRE(c.layers >= 1 && c.intermediate > 0 && c.intermediate % 64 == 0,
+               "intermediate size must be a positive multiple of 64");
   LAYA_REQUIRE(c.vocab > 0 && c.max_positions > 0 && c.type_vocab > 0, "vocab/positions/type rows must be positive");
   LAYA_REQUIRE(c.max_len > 0 && span16(c.max_len) <= (c.pos_kind == LAYA_POS_LEARNED ? span16(c.max_positions) : 1 << 20),
                "max_len exceeds the position table");
@@ -185,18 +217,63 @@ void check_config(const LayaConfig& c) {
                "act head hidden width must be a positive multiple of 64");
   LAYA_REQUIRE(c.mfma_dtype == LAYA_BF16 || c.mfma_dtype == LAYA_F16, "mfma_dtype must be LAYA_BF16 or LAYA_F16");
   LAYA_REQUIRE(c.eps > 0.f, "eps must be positive");
-  // The graded workloads run the BERT-style post-LN encoder; the reference's ModernBERT executor
-  // variant (pre-LN, RoPE, GeGLU, local windows, head layers) is not built in this library yet.
-  LAYA_REQUIRE(c.norm_order == LAYA_NORM_POST && c.pos_kind == LAYA_POS_LEARNED && c.ffn_kind == LAYA_FFN_GELU &&
-                   c.bias == 1 && c.window < 0 && c.head_layers == 0,
-               "encoder variant not built: only post-LN, learned positions, GELU FFN with biases, global "
-               "attention and head_layers=0 are implemented");
+  // Two encoder variants are built: BERT-style (post-LN, learned positions, GELU FFN with biases,
+  // global attention, no head layers) and the reference's ModernBERT executor (pre-LN, RoPE,
+  // GeGLU, no biases, local windows every layer but each global_every-th, head layers).
+  const bool bert = c.norm_order == LAYA_NORM_POST && c.pos_kind == LAYA_POS_LEARNED && c.ffn_kind == LAYA_FFN_GELU &&
+                    c.bias == 1 && c.window < 0 && c.head_layers == 0;
+  const bool modern = c.norm_order == LAYA_NORM_PRE && c.pos_kind == LAYA_POS_ROPE && c.ffn_kind == LAYA_FFN_GEGLU &&
+                      c.bias == 0 && c.global_every >= 1 && c.head_layers >= 1 && c.head_layers <= 64 &&
+                      c.theta_global > 0.f && c.theta_local > 0.f;
+  LAYA_REQUIRE(bert || modern,
+               "encoder variant not built: BERT-style (post-LN, learned positions, GELU FFN with biases, global "
+               "attention, no head layers) or ModernBERT (pre-LN, RoPE, GeGLU without biases, head layers)");
+  LAYA_REQUIRE(!modern || c.width * 4 <= 4 * 2048, "head layers need 4*width FFN rows");
+}
+
+// Checkpoint tensor table of the ModernBERT variant (the reference's, laya.py:167-190).
+void build_expected_modern(Engine& E) {
+  const LayaConfig& c = E.cfg;
+  const int64_t d = c.width, f = c.intermediate;
+  auto put = [&](const std::string& n, std::vector<int64_t> s, bool mf = false, bool gg = false) {
+    E.expected[n] = Expected{s, mf, gg};
+  };
+  put("encoder.embeddings.tok_embeddings.weight", {c.vocab, d});
+  put("encoder.embeddings.norm.weight", {d});
+  put("encoder.final_norm.weight", {d});
+  for (int i = 0; i < c.layers; ++i) {
+    const std::string p = "encoder.layers." + std::to_string(i) + ".";
+    put(p + "attn.Wqkv.weight", {3 * d, d}, true);
+    put(p + "attn.Wo.weight", {d, d}, true);
+    put(p + "mlp.Wi.weight", {2 * f, d}, true, true);
+    put(p + "mlp.Wo.weight", {d, f}, true);
+    put(p + "mlp_norm.weight", {d});
+    if (i) put(p + "attn_norm.weight", {d});
+  }
+  for (int i = 0; i < c.head_layers; ++i) {
+    const std::string p = "head.layers." + std::to_string(i) + ".";
+    put(p + "self_attn.in_proj_weight", {3 * d, d}, true);
+    put(p + "self_attn.in_proj_bias", {3 * d});
+    put(p + "self_attn.out_proj.weight", {d, d}, true);
+    put(p + "self_attn.out_proj.bias", {d});
+    put(p + "linear1.weight", {4 * d, d}, true);
+    put(p + "linear1.bias", {4 * d});
+    put(p + "linear2.weight", {d, 4 * d}, true);
+    put(p + "linear2.bias", {d});
+    put(p + "norm1.weight", {d});
+    put(p + "norm1.bias", {d});
+    put(p + "norm2.weight", {d});
+    put(p + "norm2.bias", {d});
+  }
 }
 
 void build_expected(Engine& E) {
   const LayaConfig& c = E.cfg;
   const int64_t d = c.width, f = c.intermediate;
   auto put = [&](const std::string& n, std::vector<int64_t> s, bool mf = false) { E.expected[n] = Expected{s, mf}; };
+  if (E.modern) {
+    build_expected_modern(E);
+  } else {
   put("encoder.embeddings.tok_embeddings.weight", {c.vocab, d});
   put("encoder.embeddings.position_embeddings.weight", {c.max_positions, d});
   put("encoder.embeddings.token_type_embeddings.weight", {c.type_vocab, d});
@@ -216,6 +293,7 @@ void build_expected(Engine& E) {
     put(p + "mlp.Wo.bias", {d});
     put(p + "post_mlp_norm.weight", {d});
     put(p + "post_mlp_norm.bias", {d});
+  }
   }
   put("type_emb.weight", {3, d});
   put("scorer.0.weight", {d});
@@ -258,11 +336,26 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
   s->L = make_layout(m, b, k);
   const int d = c.width, f = c.intermediate;
   try {
-    gemm_plan(m, 3 * d, d, Epi::QKV, E.cus, &s->tile[0], &s->splits[0]);
+    const int R = s->L.R;
+    gemm_plan(m, 3 * d, d, Epi::QKV, E.cus, &s->tile[0], &s->splits[0], E.modern);
     gemm_plan(m, d, d, Epi::F32, E.cus, &s->tile[1], &s->splits[1]);
-    gemm_plan(m, f, d, Epi::GELU, E.cus, &s->tile[2], &s->splits[2]);
+    if (E.modern) {
+      gemm_plan(m, 2 * f, d, Epi::GEGLU, E.cus, &s->tile[2], &s->splits[2]);
+    } else {
+      gemm_plan(m, f, d, Epi::GELU, E.cus, &s->tile[2], &s->splits[2]);
+    }
     gemm_plan(m, d, f, Epi::F32, E.cus, &s->tile[3], &s->splits[3]);
     s->splits[0] = s->splits[2] = 1;
+    if (E.modern) {  // head transformer layers: all rows, then the readout rows of the last one
+      gemm_plan(m, 3 * d, d, Epi::QKV, E.cus, &s->htile[0], &s->hsplits[0]);
+      gemm_plan(m, d, d, Epi::F32, E.cus, &s->htile[1], &s->hsplits[1]);
+      gemm_plan(m, 4 * d, d, Epi::RELU, E.cus, &s->htile[2], &s->hsplits[2]);
+      gemm_plan(m, d, 4 * d, Epi::F32, E.cus, &s->htile[3], &s->hsplits[3]);
+      gemm_plan(R, d, d, Epi::F32, E.cus, &s->htile[4], &s->hsplits[4]);
+      gemm_plan(R, 4 * d, d, Epi::RELU, E.cus, &s->htile[5], &s->hsplits[5]);
+      gemm_plan(R, d, 4 * d, Epi::F32, E.cus, &s->htile[6], &s->hsplits[6]);
+      s->hsplits[0] = s->hsplits[2] = s->hsplits[5] = 1;
+    }
     // Few 128-query tiles (batch-1 requests): split each tile's keys across waves instead of
     // sharing LDS-staged keys between query tiles, so the serial key loop is short.
     if (static_cast<long long>(m / 128) * c.heads >= 2LL * E.cus) {
@@ -280,10 +373,13 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
     s->attn_tiles = std::min(s->L.T, m / block + 2 * b + 1);
     s->head_splits = head_gemm_splits(s->L.R, d, d, E.cus);
     s->act_splits = head_gemm_splits(b, c.act_hidden, E.act_k, E.cus);
-    const int max_split = s->splits[1] > s->splits[3] ? s->splits[1] : s->splits[3];
+    const int max_split = std::max(std::max(s->splits[1], s->splits[3]), std::max(s->hsplits[1], s->hsplits[3]));
+    const int sel_split = std::max(s->hsplits[4], s->hsplits[6]);
+    const size_t ff_cols = E.modern ? std::max(f, 4 * d) : f;  // GeGLU output f; head linear1 4d
 
     const size_t h2 = 2;  // 16-bit element
-    const size_t md = static_cast<size_t>(m) * d, R = s->L.R;
+    const size_t md = static_cast<size_t>(m) * d, Rz = R;
+    const size_t rows_sel = E.modern ? Rz : 0;  // compact head-layer buffers (ModernBERT only)
     struct Part {
       void** dst;
       size_t bytes;
@@ -296,12 +392,16 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
         {&s->kk, md * h2},
         {&s->vt, md * h2},
         {&s->attn, md * h2},
-        {&s->ff, static_cast<size_t>(m) * f * h2},
+        {&s->ff, static_cast<size_t>(m) * ff_cols * h2},
         {reinterpret_cast<void**>(&s->part), md * 4 * max_split},
-        {reinterpret_cast<void**>(&s->selected), R * d * 4},
-        {reinterpret_cast<void**>(&s->normed), R * d * 4},
-        {reinterpret_cast<void**>(&s->hpart), R * d * 4 * s->head_splits},
-        {reinterpret_cast<void**>(&s->row_logit), R * 4},
+        {reinterpret_cast<void**>(&s->selected), Rz * d * 4},
+        {reinterpret_cast<void**>(&s->normed), Rz * d * 4},
+        {reinterpret_cast<void**>(&s->hpart), Rz * d * 4 * s->head_splits},
+        {reinterpret_cast<void**>(&s->row_logit), Rz * 4},
+        {&s->attn_sel, rows_sel * d * h2},
+        {&s->x_sel, rows_sel * d * h2},
+        {&s->ff_sel, rows_sel * 4 * d * h2},
+        {reinterpret_cast<void**>(&s->part_sel), rows_sel * d * 4 * sel_split},
         {reinterpret_cast<void**>(&s->feat), static_cast<size_t>(b) * E.act_k * 4},
         {reinterpret_cast<void**>(&s->apart), static_cast<size_t>(b) * c.act_hidden * 4 * s->act_splits},
         {reinterpret_cast<void**>(&s->logits), static_cast<size_t>(b) * (k + 1) * 4},
@@ -338,9 +438,11 @@ void derive_inputs(const Engine& E, Slot& s) {
   const int m = s.m, b = s.b, k = s.k;
   const int n_seq = P[L.meta], n_q = P[L.meta + 1];
   LAYA_REQUIRE(n_seq >= 0 && n_seq <= b && n_q >= 0 && n_q <= b, "sequence/question count exceeds the shape class");
+  const int positions = E.modern ? E.rope_rows : c.max_positions;  // rows of the RoPE / position table
   for (int i = 0; i < m; ++i) {
     LAYA_REQUIRE(P[L.ids + i] >= 0 && P[L.ids + i] < c.vocab, "token id out of range");
-    LAYA_REQUIRE(P[L.positions + i] >= 0 && P[L.positions + i] < c.max_positions, "position out of range");
+    LAYA_REQUIRE(P[L.positions + i] >= 0 && P[L.positions + i] < positions, "position out of range");
+    LAYA_REQUIRE(!E.modern || (P[L.kinds + i] >= 0 && P[L.kinds + i] < 3), "question kind out of range");
   }
   // Attention tiles: sequences in increasing start order, 16-aligned, non-overlapping.
   for (int sq = 0; sq < n_seq; ++sq) {
@@ -375,28 +477,47 @@ void check_launch(hipError_t e, const char* what) {
 }
 
 // The forward as a list of launches ("stages"); forward() runs them in order, and the timing
-// entry point replays one of them in isolation.
+// entry point replays one of them in isolation.  Encoder stages repeat per encoder layer, head
+// stages (ModernBERT variant) per head transformer layer.
 enum Stage : int {
   kEmbed = 0, kQkv, kAttention, kAttnOut, kAttnNorm, kFfnUp, kFfnDown, kFfnNorm,
+  kTypeNorm, kHlQkv, kHlAttention, kHlGather, kHlOut, kHlNorm2, kHlUp, kHlDown, kHlNorm,
   kHeadGather, kHeadScorer, kHeadLogit, kHeadFeatures, kActHidden, kActOut, kStageCount
 };
 const char* const kStageNames[kStageCount] = {
     "embed_norm", "qkv", "attention", "attn_out", "attn_norm", "ffn_up", "ffn_down", "ffn_norm",
-    "head_gather", "head_scorer", "head_logit", "head_features", "act_hidden", "act_out"};
+    "type_norm", "head_qkv", "head_attention", "head_gather_rows", "head_out", "head_norm2", "head_up",
+    "head_down", "head_norm", "head_gather", "head_scorer", "head_logit", "head_features", "act_hidden", "act_out"};
 bool per_layer(int stage) { return stage >= kQkv && stage <= kFfnNorm; }
+bool per_head_layer(int stage) { return stage >= kHlQkv && stage <= kHlNorm; }
+// Whether a stage belongs to this engine's forward (for layer `layer` of its kind).
+bool stage_used(const Engine& E, int stage, int layer) {
+  if (per_layer(stage)) return layer >= 0 && layer < E.cfg.layers;
+  if (per_head_layer(stage)) {
+    const int last = E.cfg.head_layers - 1;
+    return E.modern && layer >= 0 && layer <= last && (stage != kHlGather || layer == last);
+  }
+  if (stage == kTypeNorm) return E.modern;
+  if (stage == kHeadGather) return !E.modern;
+  return stage >= 0 && stage < kStageCount;
+}
 
 void launch_stage(Engine& E, Slot& s, int stage, int layer) {
   const LayaConfig& c = E.cfg;
-  const int m = s.m, d = c.width, f = c.intermediate;
+  const int m = s.m, d = c.width, f = c.intermediate, R = s.L.R;
   const DType t = E.mfma();
   const int32_t* P = s.d_packed;
   const Layout& L = s.L;
   hipStream_t st = E.stream;
-  const long long md = static_cast<long long>(m) * d;
+  const long long md = static_cast<long long>(m) * d, rd = static_cast<long long>(R) * d;
   const Layer* ly = per_layer(stage) ? &E.layers[layer] : nullptr;
+  const HeadLayer* hl = per_head_layer(stage) ? &E.head_layers[layer] : nullptr;
+  const bool last_head = hl && layer == c.head_layers - 1;
   GemmArgs g{};
   switch (stage) {
     case kEmbed: {
+      // BERT-style: + position row + type row 0, LN with bias.  ModernBERT: token row, LN without
+      // bias; layer 0 has no attention norm, so x is the normalised embedding itself.
       EmbedArgs ea{P + L.ids, P + L.positions, E.tok, E.pos, E.type0, E.emb_g, E.emb_b, c.eps,
                    s.residual, s.x, m, c.vocab, c.max_positions};
       check_launch(launch_embed(ea, d, t, st), "embed");
@@ -405,10 +526,16 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
     case kQkv:
       g.a = s.x; g.b = ly->wqkv; g.M = m; g.N = 3 * d; g.K = d; g.lda = d; g.ldb = d;
       g.bias = ly->bqkv; g.splits = 1; g.q = s.q; g.k = s.kk; g.vt = s.vt; g.width = d;
+      if (E.modern) {
+        const size_t table = static_cast<size_t>(E.rope_rows) * 32;
+        g.rope_cos = E.rope + (ly->local ? 2 : 0) * table;
+        g.rope_sin = g.rope_cos + table;
+        g.positions = P + L.positions;
+      }
       check_launch(launch_gemm(g, Epi::QKV, t, s.tile[0], st), "qkv");
       break;
     case kAttention: {
-      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, m, c.heads, s.attn_tiles};
+      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, m, c.heads, s.attn_tiles, ly->local ? c.window : -1};
       check_launch(launch_attention(aa, t, s.attn_mode, s.attn_waves, st), "attention");
       break;
     }
@@ -418,14 +545,19 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       check_launch(launch_gemm(g, Epi::F32, t, s.tile[1], st), "attn out");
       break;
     case kAttnNorm: {
-      AddNormArgs na{s.residual, s.part, s.splits[1], md, ly->bo, ly->n1g, ly->n1b, c.eps, nullptr, s.residual, s.x, m};
-      check_launch(launch_add_norm(na, d, t, st), "post-attention norm");
+      // BERT-style: residual = LN(residual + branch + bias).  ModernBERT (pre-LN):
+      // residual += branch, x = mlp_norm(residual).
+      AddNormArgs na = E.modern
+          ? AddNormArgs{s.residual, s.part, s.splits[1], md, nullptr, ly->n2g, nullptr, c.eps, s.residual, nullptr, s.x, m}
+          : AddNormArgs{s.residual, s.part, s.splits[1], md, ly->bo, ly->n1g, ly->n1b, c.eps, nullptr, s.residual, s.x, m};
+      check_launch(launch_add_norm(na, d, t, st), "attention norm");
       break;
     }
     case kFfnUp:
-      g.a = s.x; g.b = ly->wi; g.M = m; g.N = f; g.K = d; g.lda = d; g.ldb = d;
-      g.bias = ly->bi; g.out = s.ff; g.ldo = f; g.splits = 1;
-      check_launch(launch_gemm(g, Epi::GELU, t, s.tile[2], st), "ffn up");
+      g.a = s.x; g.b = ly->wi; g.M = m; g.K = d; g.lda = d; g.ldb = d; g.bias = ly->bi; g.out = s.ff;
+      g.ldo = f; g.splits = 1;
+      g.N = E.modern ? 2 * f : f;
+      check_launch(launch_gemm(g, E.modern ? Epi::GEGLU : Epi::GELU, t, s.tile[2], st), "ffn up");
       break;
     case kFfnDown:
       g.a = s.ff; g.b = ly->wo2; g.M = m; g.N = d; g.K = f; g.lda = f; g.ldb = f;
@@ -433,8 +565,93 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       check_launch(launch_gemm(g, Epi::F32, t, s.tile[3], st), "ffn down");
       break;
     case kFfnNorm: {
-      AddNormArgs na{s.residual, s.part, s.splits[3], md, ly->bo2, ly->n2g, ly->n2b, c.eps, nullptr, s.residual, s.x, m};
-      check_launch(launch_add_norm(na, d, t, st), "post-ffn norm");
+      AddNormArgs na{};
+      if (!E.modern) {
+        na = AddNormArgs{s.residual, s.part, s.splits[3], md, ly->bo2, ly->n2g, ly->n2b, c.eps, nullptr, s.residual, s.x, m};
+      } else if (layer + 1 < c.layers) {  // residual += branch, x = next layer's attn_norm(residual)
+        na = AddNormArgs{s.residual, s.part, s.splits[3], md, nullptr, E.layers[layer + 1].n1g, nullptr, c.eps,
+                         s.residual, nullptr, s.x, m};
+      } else {  // last layer: residual = final_norm(residual + branch), in place (runtime.py:107-109)
+        na = AddNormArgs{s.residual, s.part, s.splits[3], md, nullptr, E.final_norm, nullptr, c.eps, nullptr,
+                         s.residual, nullptr, m};
+      }
+      check_launch(launch_add_norm(na, d, t, st), "ffn norm");
+      break;
+    }
+    case kTypeNorm: {  // residual += type_emb[kind of each row] (laya.py:218), x = norm1 of head layer 0
+      const HeadLayer& h0 = E.head_layers[0];
+      AddNormArgs na{s.residual, nullptr, 1, 0, nullptr, h0.n1g, h0.n1b, 1e-5f, s.residual, nullptr, s.x, m,
+                     E.type_emb, P + L.kinds};
+      check_launch(launch_add_norm(na, d, t, st), "type norm");
+      break;
+    }
+    case kHlQkv:
+      g.a = s.x; g.b = hl->in_w; g.M = m; g.N = 3 * d; g.K = d; g.lda = d; g.ldb = d;
+      g.bias = hl->in_b; g.splits = 1; g.q = s.q; g.k = s.kk; g.vt = s.vt; g.width = d;
+      check_launch(launch_gemm(g, Epi::QKV, t, s.htile[0], st), "head in_proj");
+      break;
+    case kHlAttention: {
+      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, m, c.heads, s.attn_tiles, -1};
+      check_launch(launch_attention(aa, t, s.attn_mode, s.attn_waves, st), "head attention");
+      break;
+    }
+    case kHlGather: {  // last head layer: only the readout rows go on (laya.py:225-228)
+      GatherRowsArgs ga{s.residual, s.selected, s.attn, s.attn_sel, P + L.sel_src, P + L.n_sel, R};
+      check_launch(launch_gather_rows(ga, d, t, st), "head gather rows");
+      break;
+    }
+    case kHlOut:
+      g.b = hl->out_w; g.N = d; g.K = d; g.lda = d; g.ldb = d; g.ldo = d;
+      if (last_head) {
+        g.a = s.attn_sel; g.M = R; g.out = s.part_sel; g.split_stride = rd; g.splits = s.hsplits[4];
+        check_launch(launch_gemm(g, Epi::F32, t, s.htile[4], st), "head out_proj");
+      } else {
+        g.a = s.attn; g.M = m; g.out = s.part; g.split_stride = md; g.splits = s.hsplits[1];
+        check_launch(launch_gemm(g, Epi::F32, t, s.htile[1], st), "head out_proj");
+      }
+      break;
+    case kHlNorm2: {  // residual += out_proj(attention) + bias, x = norm2(residual)
+      AddNormArgs na = last_head
+          ? AddNormArgs{s.selected, s.part_sel, s.hsplits[4], rd, hl->out_b, hl->n2g, hl->n2b, 1e-5f, s.selected,
+                        nullptr, s.x_sel, R}
+          : AddNormArgs{s.residual, s.part, s.hsplits[1], md, hl->out_b, hl->n2g, hl->n2b, 1e-5f, s.residual,
+                        nullptr, s.x, m};
+      check_launch(launch_add_norm(na, d, t, st), "head norm2");
+      break;
+    }
+    case kHlUp:
+      g.b = hl->l1_w; g.N = 4 * d; g.K = d; g.lda = d; g.ldb = d; g.bias = hl->l1_b; g.ldo = 4 * d; g.splits = 1;
+      if (last_head) {
+        g.a = s.x_sel; g.M = R; g.out = s.ff_sel;
+        check_launch(launch_gemm(g, Epi::RELU, t, s.htile[5], st), "head linear1");
+      } else {
+        g.a = s.x; g.M = m; g.out = s.ff;
+        check_launch(launch_gemm(g, Epi::RELU, t, s.htile[2], st), "head linear1");
+      }
+      break;
+    case kHlDown:
+      g.b = hl->l2_w; g.N = d; g.K = 4 * d; g.lda = 4 * d; g.ldb = 4 * d; g.ldo = d;
+      if (last_head) {
+        g.a = s.ff_sel; g.M = R; g.out = s.part_sel; g.split_stride = rd; g.splits = s.hsplits[6];
+        check_launch(launch_gemm(g, Epi::F32, t, s.htile[6], st), "head linear2");
+      } else {
+        g.a = s.ff; g.M = m; g.out = s.part; g.split_stride = md; g.splits = s.hsplits[3];
+        check_launch(launch_gemm(g, Epi::F32, t, s.htile[3], st), "head linear2");
+      }
+      break;
+    case kHlNorm: {
+      // residual += linear2(...) + bias; then the next head layer's norm1, or - after the last
+      // layer, on the readout rows - the scorer's LayerNorm (scorer.0, fp32 rows for its GEMM).
+      AddNormArgs na{};
+      if (last_head) {
+        na = AddNormArgs{s.selected, s.part_sel, s.hsplits[6], rd, hl->l2_b, E.s0w, E.s0b, 1e-5f, s.selected,
+                         s.normed, nullptr, R};
+      } else {
+        const HeadLayer& nx = E.head_layers[layer + 1];
+        na = AddNormArgs{s.residual, s.part, s.hsplits[3], md, hl->l2_b, nx.n1g, nx.n1b, 1e-5f, s.residual,
+                         nullptr, s.x, m};
+      }
+      check_launch(launch_add_norm(na, d, t, st), "head norm");
       break;
     }
     case kHeadGather: {
@@ -449,9 +666,9 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       break;
     }
     case kHeadLogit: {
-      HeadLogitArgs hl{s.hpart, s.head_splits, static_cast<long long>(L.R) * d, E.s1b, E.s3w, E.s3b,
-                       P + L.sel_q, P + L.qoff, P + L.n_sel, s.row_logit, s.logits, L.R, s.k};
-      check_launch(launch_head_logit(hl, d, st), "head logit");
+      HeadLogitArgs hlg{s.hpart, s.head_splits, static_cast<long long>(L.R) * d, E.s1b, E.s3w, E.s3b,
+                        P + L.sel_q, P + L.qoff, P + L.n_sel, s.row_logit, s.logits, L.R, s.k};
+      check_launch(launch_head_logit(hlg, d, st), "head logit");
       break;
     }
     case kHeadFeatures: {
@@ -481,7 +698,75 @@ void forward(Engine& E, Slot& s) {
   launch_stage(E, s, kEmbed, 0);
   for (int i = 0; i < E.cfg.layers; ++i)
     for (int stage = kQkv; stage <= kFfnNorm; ++stage) launch_stage(E, s, stage, i);
-  for (int stage = kHeadGather; stage < kStageCount; ++stage) launch_stage(E, s, stage, 0);
+  if (E.modern) {
+    launch_stage(E, s, kTypeNorm, 0);
+    for (int j = 0; j < E.cfg.head_layers; ++j)
+      for (int stage = kHlQkv; stage <= kHlNorm; ++stage)
+        if (stage_used(E, stage, j)) launch_stage(E, s, stage, j);
+  } else {
+    launch_stage(E, s, kHeadGather, 0);
+  }
+  for (int stage = kHeadScorer; stage < kStageCount; ++stage) launch_stage(E, s, stage, 0);
+}
+
+// ModernBERT variant: layer tables and the RoPE cos/sin tables of both thetas (runtime.py:159-165:
+// freq_i = 1 / theta^(2i/64), angle = position * freq_i), over every position a packed row can hold.
+void finalize_modern(Engine& E) {
+  const LayaConfig& c = E.cfg;
+  E.final_norm = f32(E, "encoder.final_norm.weight");
+  E.pos = nullptr;
+  E.type0 = nullptr;
+  E.emb_b = nullptr;
+  for (int i = 0; i < c.layers; ++i) {
+    const std::string p = "encoder.layers." + std::to_string(i) + ".";
+    Layer ly{};
+    ly.wqkv = need(E, p + "attn.Wqkv.weight").ptr;
+    ly.wo = need(E, p + "attn.Wo.weight").ptr;
+    ly.wi = need(E, p + "mlp.Wi.weight").ptr;
+    ly.wo2 = need(E, p + "mlp.Wo.weight").ptr;
+    ly.n1g = i ? f32(E, p + "attn_norm.weight") : nullptr;
+    ly.n2g = f32(E, p + "mlp_norm.weight");
+    ly.local = i % c.global_every != 0;
+    E.layers.push_back(ly);
+  }
+  for (int i = 0; i < c.head_layers; ++i) {
+    const std::string p = "head.layers." + std::to_string(i) + ".";
+    HeadLayer h{};
+    h.in_w = need(E, p + "self_attn.in_proj_weight").ptr;
+    h.in_b = f32(E, p + "self_attn.in_proj_bias");
+    h.out_w = need(E, p + "self_attn.out_proj.weight").ptr;
+    h.out_b = f32(E, p + "self_attn.out_proj.bias");
+    h.l1_w = need(E, p + "linear1.weight").ptr;
+    h.l1_b = f32(E, p + "linear1.bias");
+    h.l2_w = need(E, p + "linear2.weight").ptr;
+    h.l2_b = f32(E, p + "linear2.bias");
+    h.n1g = f32(E, p + "norm1.weight");
+    h.n1b = f32(E, p + "norm1.bias");
+    h.n2g = f32(E, p + "norm2.weight");
+    h.n2b = f32(E, p + "norm2.bias");
+    E.head_layers.push_back(h);
+  }
+  const int rows = span16(c.max_len);
+  std::vector<float> tables(static_cast<size_t>(4) * rows * 32);
+  const float theta[2] = {c.theta_global, c.theta_local};
+  for (int t = 0; t < 2; ++t)
+    for (int i = 0; i < 32; ++i) {
+      const float freq = 1.0f / std::pow(theta[t], static_cast<float>(2 * i) / 64.0f);
+      for (int p = 0; p < rows; ++p) {
+        const float angle = static_cast<float>(p) * freq;
+        tables[(static_cast<size_t>(2 * t) * rows + p) * 32 + i] = std::cos(angle);
+        tables[(static_cast<size_t>(2 * t + 1) * rows + p) * 32 + i] = std::sin(angle);
+      }
+    }
+  if (E.rope) {
+    (void)hipFree(E.rope);
+    E.weight_bytes -= static_cast<size_t>(4) * E.rope_rows * 32 * 4;
+    E.rope = nullptr;
+  }
+  LAYA_HIP(hipMalloc(reinterpret_cast<void**>(&E.rope), tables.size() * 4));
+  E.rope_rows = rows;
+  E.weight_bytes += tables.size() * 4;
+  LAYA_HIP(hipMemcpy(E.rope, tables.data(), tables.size() * 4, hipMemcpyHostToDevice));
 }
 
 Slot* find_slot(Engine& E, int m, int b, int k, bool* miss) {
@@ -570,6 +855,7 @@ int laya_create(const LayaConfig* cfg, int device, int max_slots, void** handle)
                  std::string(prop.name) + " is " + prop.gcnArchName + "; liblaya_hip is built for gfx950 (MI355X)");
     E->cus = prop.multiProcessorCount;
     E->act_k = (cfg->width + 4 + 255) / 256 * 256;
+    E->modern = cfg->norm_order == LAYA_NORM_PRE;
     prepare_device();
     LAYA_HIP(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
     build_expected(*E);
@@ -618,6 +904,15 @@ int laya_load_weight(void* handle, const char* name, const void* host_data, int 
           o[i] = bf ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
         }
       }
+      if (it->second.geglu) {  // interleave gate and value rows (geglu_row)
+        const int64_t rows = shape[0], cols = shape[1], f = rows / 2;
+        LAYA_REQUIRE(f % 16 == 0, "GeGLU intermediate size must be a multiple of 16: " + n);
+        std::vector<uint16_t> inter(count);
+        for (int64_t r = 0; r < rows; ++r)
+          std::memcpy(&inter[static_cast<size_t>(r) * cols], &o[static_cast<size_t>(geglu_row(r, f)) * cols], cols * 2);
+        std::memcpy(o, inter.data(), t.bytes);
+        t.geglu = true;
+      }
       src = staged.data();
     } else {
       t.dtype = DType::F32;
@@ -649,11 +944,15 @@ int laya_finalize(void* handle) {
   return guarded(E, [&] {
     for (auto& kv : E->expected) LAYA_REQUIRE(E->weights.count(kv.first), "missing tensor: " + kv.first);
     E->tok = f32(*E, "encoder.embeddings.tok_embeddings.weight");
+    E->emb_g = f32(*E, "encoder.embeddings.norm.weight");
+    E->layers.clear();
+    E->head_layers.clear();
+    if (E->modern) {
+      finalize_modern(*E);
+    } else {
     E->pos = f32(*E, "encoder.embeddings.position_embeddings.weight");
     E->type0 = f32(*E, "encoder.embeddings.token_type_embeddings.weight");
-    E->emb_g = f32(*E, "encoder.embeddings.norm.weight");
     E->emb_b = f32(*E, "encoder.embeddings.norm.bias");
-    E->layers.clear();
     for (int i = 0; i < E->cfg.layers; ++i) {
       const std::string p = "encoder.layers." + std::to_string(i) + ".";
       Layer ly;
@@ -669,7 +968,9 @@ int laya_finalize(void* handle) {
       ly.bo2 = f32(*E, p + "mlp.Wo.bias");
       ly.n2g = f32(*E, p + "post_mlp_norm.weight");
       ly.n2b = f32(*E, p + "post_mlp_norm.bias");
+      ly.local = false;
       E->layers.push_back(ly);
+    }
     }
     E->type_emb = f32(*E, "type_emb.weight");
     E->s0w = f32(*E, "scorer.0.weight");
@@ -782,7 +1083,7 @@ int laya_time_stage(void* handle, const int32_t* host_packed, const LayaShape* s
   return guarded(E, [&] {
     LAYA_REQUIRE(avg_ms && reps >= 1 && reps <= 100000, "reps must be in [1, 100000]");
     LAYA_REQUIRE(stage >= 0 && stage < kStageCount, "unknown stage");
-    LAYA_REQUIRE(!per_layer(stage) || (layer >= 0 && layer < E->cfg.layers), "layer out of range");
+    LAYA_REQUIRE(stage_used(*E, stage, layer), "stage or layer not in this model's forward");
     bool miss = false;
     Slot* s = stage_inputs(E, host_packed, shape, &miss);
     forward(*E, *s);  // every buffer the stage reads now holds this request's values
@@ -811,8 +1112,12 @@ int laya_read_weight(void* handle, const char* name, float* host_out, int64_t co
     } else {
       std::vector<uint16_t> raw(t.count);
       LAYA_HIP(hipMemcpy(raw.data(), t.ptr, t.bytes, hipMemcpyDeviceToHost));
-      for (size_t i = 0; i < t.count; ++i)
-        host_out[i] = t.dtype == DType::BF16 ? bf16_bits_to_f32(raw[i]) : f16_bits_to_f32(raw[i]);
+      const int64_t cols = t.shape.size() == 2 ? t.shape[1] : 1, f = t.shape.empty() ? 0 : t.shape[0] / 2;
+      for (size_t i = 0; i < t.count; ++i) {
+        // resident element i sits at checkpoint row geglu_row(row) for interleaved matrices
+        const size_t dst = t.geglu ? static_cast<size_t>(geglu_row(static_cast<int64_t>(i) / cols, f)) * cols + i % cols : i;
+        host_out[dst] = t.dtype == DType::BF16 ? bf16_bits_to_f32(raw[i]) : f16_bits_to_f32(raw[i]);
+      }
     }
   });
 }
@@ -837,6 +1142,7 @@ int laya_destroy(void* handle) {
   for (auto& kv : E->weights) (void)hipFree(kv.second.ptr);
   E->weights.clear();
   if (E->a0w_pad) (void)hipFree(E->a0w_pad);
+  if (E->rope) (void)hipFree(E->rope);
   if (E->stream) (void)hipStreamDestroy(E->stream);
   delete E;
   return LAYA_OK;
@@ -885,8 +1191,10 @@ int laya_op_linear(const void* x, const void* w, const float* bias, void* out, i
                    int K, int splits, int tile, void* stream) {
   return guarded(nullptr, [&] {
     prepare_device();
-    LAYA_REQUIRE(kind >= 0 && kind <= 2, "kind must be 0 (fp32), 1 (16-bit) or 2 (16-bit GELU)");
-    const Epi epi = kind == 0 ? Epi::F32 : kind == 1 ? Epi::HALF : Epi::GELU;
+    LAYA_REQUIRE(kind >= 0 && kind <= 4,
+                 "kind must be 0 (fp32), 1 (16-bit), 2 (16-bit GELU), 3 (16-bit ReLU) or 4 (16-bit GeGLU)");
+    const Epi epi = kind == 0 ? Epi::F32 : kind == 1 ? Epi::HALF : kind == 2 ? Epi::GELU : kind == 3 ? Epi::RELU
+                                                                                                    : Epi::GEGLU;
     int cus = 256;
     if (tile < 0) {
       gemm_plan(M, N, K, epi, cus, &tile, &splits);
@@ -895,35 +1203,40 @@ int laya_op_linear(const void* x, const void* w, const float* bias, void* out, i
     LAYA_REQUIRE(tile < gemm_tile_count(), "bad tile id");
     LAYA_REQUIRE(K % 64 == 0 && N % gemm_tile(tile).bn == 0, "K must be a multiple of 64 and N of the tile width");
     GemmArgs g{};
-    g.a = x; g.b = w; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldb = K; g.bias = bias; g.out = out; g.ldo = N;
+    g.a = x; g.b = w; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldb = K; g.bias = bias; g.out = out;
+    g.ldo = epi == Epi::GEGLU ? N / 2 : N;
     g.split_stride = static_cast<long long>(M) * N; g.splits = splits < 1 ? 1 : splits;
     check_launch(launch_gemm(g, epi, half_type(dtype16), tile, static_cast<hipStream_t>(stream)), "linear");
   });
 }
 
-int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* k, void* vt, int dtype16, int M,
-                int width, int tile, void* stream) {
+int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* k, void* vt, const float* rope_cos,
+                const float* rope_sin, const int32_t* positions, int dtype16, int M, int width, int tile,
+                void* stream) {
   return guarded(nullptr, [&] {
     prepare_device();
     int splits = 1;
-    if (tile < 0) gemm_plan(M, 3 * width, width, Epi::QKV, 256, &tile, &splits);
+    const bool rope = rope_cos != nullptr;
+    LAYA_REQUIRE(!rope || (rope_sin && positions), "RoPE needs cos, sin and positions");
+    if (tile < 0) gemm_plan(M, 3 * width, width, Epi::QKV, 256, &tile, &splits, rope);
     LAYA_REQUIRE(tile < gemm_tile_count(), "bad tile id");
     LAYA_REQUIRE(width % 64 == 0 && (3 * width) % gemm_tile(tile).bn == 0, "width does not fit the tile");
     GemmArgs g{};
     g.a = x; g.b = w; g.M = M; g.N = 3 * width; g.K = width; g.lda = width; g.ldb = width; g.bias = bias;
     g.splits = 1; g.q = q; g.k = k; g.vt = vt; g.width = width;
+    g.rope_cos = rope_cos; g.rope_sin = rope_sin; g.positions = positions;
     check_launch(launch_gemm(g, Epi::QKV, half_type(dtype16), tile, static_cast<hipStream_t>(stream)), "qkv");
   });
 }
 
 int laya_op_attention(const void* q, const void* k, const void* vt, void* out, const int32_t* tiles, int m,
-                      int heads, int max_tiles, int mode, int waves, int dtype16, void* stream) {
+                      int heads, int max_tiles, int mode, int waves, int window, int dtype16, void* stream) {
   return guarded(nullptr, [&] {
     LAYA_REQUIRE(attention_mode_valid(mode, waves),
                  "mode 0 (shared K/V) takes 1, 2, 4 or 8 waves; mode 1 (split keys) takes 2 or 4");
     LAYA_REQUIRE(m % 16 == 0, "rows must be a multiple of 16");
     LAYA_REQUIRE((reinterpret_cast<uintptr_t>(tiles) & 15) == 0, "tile list must be 16-byte aligned");
-    AttnArgs a{q, k, vt, out, tiles, m, heads, max_tiles};
+    AttnArgs a{q, k, vt, out, tiles, m, heads, max_tiles, window < 0 ? -1 : window};
     check_launch(launch_attention(a, half_type(dtype16), mode, waves, static_cast<hipStream_t>(stream)),
                  "attention");
   });

@@ -16,10 +16,10 @@ FFN_GELU, FFN_GEGLU = 0, 1
 
 
 class LayaConfig(ct.Structure):
-    _fields_ = [(name, ct.c_float if name == "eps" else ct.c_int32) for name in (
+    _fields_ = [(name, ct.c_float if name in ("eps", "theta_global", "theta_local") else ct.c_int32) for name in (
         "width", "heads", "layers", "intermediate", "vocab", "max_positions", "type_vocab",
         "norm_order", "pos_kind", "ffn_kind", "bias", "eps", "window", "global_every",
-        "head_layers", "n_act", "act_hidden", "max_len", "mfma_dtype")]
+        "head_layers", "n_act", "act_hidden", "max_len", "mfma_dtype", "theta_global", "theta_local")]
 
 
 class LayaShape(ct.Structure):
@@ -55,8 +55,8 @@ SIGNATURES = {
     "laya_op_embed": ([_p, _p, _p, _p, _p, _p, _p, _f, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "laya_op_norm": ([_p, _p, _i, _i64, _p, _p, _p, _f, _p, _p, _p, _i, _i, _i, _p], _i),
     "laya_op_linear": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p], _i),
-    "laya_op_qkv": ([_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p], _i),
-    "laya_op_attention": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p], _i),
+    "laya_op_qkv": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p], _i),
+    "laya_op_attention": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p], _i),
 }
 
 _lib = None

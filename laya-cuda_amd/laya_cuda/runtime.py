@@ -133,7 +133,9 @@ def _config(adapter):
         ffn_kind=_lib.FFN_GELU if bert else _lib.FFN_GEGLU, bias=int(bert), eps=adapter.eps,
         window=adapter.window if not bert else -1, global_every=adapter.global_every,
         head_layers=adapter.head_layers, n_act=adapter.n_act, act_hidden=adapter.act_hidden,
-        max_len=adapter.max_len, mfma_dtype=_lib.F16 if precision == "float16" else _lib.BF16)
+        max_len=adapter.max_len, mfma_dtype=_lib.F16 if precision == "float16" else _lib.BF16,
+        theta_global=adapter.theta[0] if adapter.theta else 0.0,
+        theta_local=adapter.theta[1] if len(adapter.theta) > 1 else 0.0)
 
 
 def _host_dtype(array):
@@ -200,6 +202,13 @@ class Runtime:
             raise RuntimeError("Runtime is closed")
         if not questions:
             raise ValueError("Provide at least one question")
+        if self.adapter.head_layers:
+            # Head transformer layers add each token's question-type row to the whole sequence
+            # (laya.py:218), so a sequence can carry questions of one type only.
+            kinds = {}
+            for seq, _, kind in questions:
+                if kinds.setdefault(seq, kind) != kind:
+                    raise ValueError("With head transformer layers, questions sharing a sequence must share its type")
         key = key or shape_class(sequences, questions)
         block = pack(sequences, questions, key, self.adapter.pad, self.adapter.vocab)
         m, b, k = key

@@ -40,6 +40,26 @@ def task_config(max_len, mfma_dtype="float16"):
             "temperature": [1, 1, 1], "mfma_dtype": mfma_dtype}
 
 
+def modernbert_config(layers, width, heads, intermediate, vocab, positions, global_every=3, local_attention=128,
+                      global_theta=160000.0, local_theta=10000.0, eps=1e-5):
+    """encoder/config.json of a ModernBERT/mmBERT encoder (the reference executor's variant)."""
+    return {"model_type": "modernbert", "hidden_size": width, "num_attention_heads": heads,
+            "num_hidden_layers": layers, "intermediate_size": intermediate, "vocab_size": vocab,
+            "max_position_embeddings": positions, "global_attn_every_n_layers": global_every,
+            "local_attention": local_attention, "global_rope_theta": global_theta, "local_rope_theta": local_theta,
+            "norm_eps": eps, "norm_bias": False, "attention_bias": False, "mlp_bias": False,
+            "hidden_activation": "gelu", "pad_token_id": 0}
+
+
+def modernbert_adapter(*, layers, width, heads, intermediate, vocab, positions, max_len, head_layers=1,
+                       mfma_dtype="float16", **config):
+    """Checkpoint-less adapter of the ModernBERT variant with `head_layers` head transformer layers."""
+    task = task_config(max_len, mfma_dtype)
+    task["head_layers"] = head_layers
+    return Laya.from_configs(modernbert_config(layers, width, heads, intermediate, vocab, positions, **config),
+                             task, pad=0)
+
+
 def adapter(name=None, *, mfma_dtype="float16", **overrides):
     """Checkpoint-less adapter for a named workload (or explicit sizes)."""
     spec = dict(WORKLOADS[name]) if name else {}

@@ -100,11 +100,17 @@ def test_create_without_gpu_reports_an_error():
 
 
 def test_create_rejects_unbuilt_variants_before_touching_the_device():
+    """Only the two built variants pass: BERT-style and the reference's ModernBERT executor.  A mix
+    (pre-LN with learned positions) or a ModernBERT config without RoPE thetas is rejected."""
     lib = _lib.load()
     cfg = _lib.LayaConfig(width=64, heads=1, layers=1, intermediate=256, vocab=10, max_positions=16, type_vocab=2,
-                          norm_order=1, pos_kind=1, ffn_kind=1, bias=0, eps=1e-5, window=64, global_every=3,
-                          head_layers=1, n_act=2, act_hidden=256, max_len=16, mfma_dtype=_lib.F16)
+                          norm_order=1, pos_kind=0, ffn_kind=1, bias=0, eps=1e-5, window=64, global_every=3,
+                          head_layers=1, n_act=2, act_hidden=256, max_len=16, mfma_dtype=_lib.F16,
+                          theta_global=160000.0, theta_local=10000.0)
     handle = ct.c_void_p()
+    assert lib.laya_create(ct.byref(cfg), 0, 4, ct.byref(handle)) == _lib.EINVAL
+    assert "variant not built" in _lib.error(None)
+    cfg.pos_kind, cfg.theta_local = 1, 0.0
     assert lib.laya_create(ct.byref(cfg), 0, 4, ct.byref(handle)) == _lib.EINVAL
     assert "variant not built" in _lib.error(None)
     cfg.norm_order, cfg.pos_kind, cfg.ffn_kind, cfg.bias, cfg.window, cfg.head_layers = 0, 0, 0, 1, -1, 0

@@ -235,7 +235,8 @@ def test_qkv_epilogue_writes_head_major_layout(gpu, tile):
     # Keep every operand referenced until the kernel has run: a temporary freed inside the argument
     # list returns its memory to torch's caching allocator, which hands it to the next operand.
     d_x, d_w, d_bias = to16(x, "f16", gpu), to16(w, "f16", gpu), dev(bias, gpu)
-    check(_lib.load().laya_op_qkv(p(d_x), p(d_w), p(d_bias), p(q), p(k), p(vt), _lib.F16, M, width, tile, stream()))
+    check(_lib.load().laya_op_qkv(p(d_x), p(d_w), p(d_bias), p(q), p(k), p(vt), None, None, None, _lib.F16, M, width,
+                                  tile, stream()))
     sync()
     full = x @ w.T + bias  # [M, 3*width], exact in fp32 and fp16
     parts = full.reshape(M, 3, heads, 64)
@@ -276,7 +277,7 @@ def test_packed_attention_matches_float64(gpu, lengths, dtype, mode, waves):
     args = [to16(a, dtype, gpu) for a in (q, k, vt)] + [out, dev(tiles, gpu)]
 
     def run():
-        check(lib.laya_op_attention(*[p(a) for a in args], m, h, max_tiles, mode, waves, DTYPES[dtype][0], stream()))
+        check(lib.laya_op_attention(*[p(a) for a in args], m, h, max_tiles, mode, waves, -1, DTYPES[dtype][0], stream()))
         sync()
         return from16(out)
 
@@ -294,3 +295,115 @@ def test_packed_attention_matches_float64(gpu, lengths, dtype, mode, waves):
         expected = (pr @ vv).transpose(1, 0, 2).reshape(n_tok, h * 64)
         np.testing.assert_allclose(eager[start:start + n_tok], expected, atol=atol, rtol=rtol)
     np.testing.assert_array_equal(eager[~real], 0)
+
+
+# ---------------- ModernBERT-variant epilogues and local attention ----------------
+
+def geglu_order(f):
+    """Checkpoint row held by each resident row of a [2f][K] GeGLU matrix (32-row groups:
+    16 gate rows, then their 16 value rows)."""
+    r = np.arange(2 * f)
+    group, within = r // 32, r % 32
+    return np.where(within < 16, group * 16 + within, f + group * 16 + within - 16)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_linear_relu_epilogue(gpu, dtype):
+    t = torch()
+    rng = np.random.default_rng(21)
+    M, N, K = 96, 512, 256
+    x = half_round(rng.normal(0, 1, (M, K)), dtype)
+    w = half_round(rng.normal(0, 1 / math.sqrt(K), (N, K)), dtype)
+    bias = rng.normal(0, .5, N).astype(np.float32)
+    d_x, d_w, d_b = to16(x, dtype, gpu), to16(w, dtype, gpu), dev(bias, gpu)
+    out = t.empty((M, N), dtype=t.float16 if dtype == "f16" else t.bfloat16, device=gpu)
+    linear(d_x, d_w, d_b, out, 3, dtype, M, N, K, 1, -1)
+    expected = np.maximum(x.astype(np.float64) @ w.T.astype(np.float64) + bias, 0)
+    tol = 2e-3 if dtype == "f16" else 1e-2
+    np.testing.assert_allclose(from16(out), expected, atol=tol, rtol=tol)
+    assert (from16(out) >= 0).all()
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+@pytest.mark.parametrize("tile", [-1, 2, 5, 7])
+def test_linear_geglu_epilogue_on_interleaved_rows(gpu, dtype, tile):
+    """gelu(x Wg^T) * (x Wv^T) (activate mode 2, kernels.cu:62-66) from one GEMM over the
+    interleaved [2f][K] matrix; output [M][f] in feature order."""
+    t = torch()
+    rng = np.random.default_rng(22)
+    M, f, K = 128, 1152, 256
+    x = half_round(rng.normal(0, 1, (M, K)), dtype)
+    w = half_round(rng.normal(0, 1.5 / math.sqrt(K), (2 * f, K)), dtype)  # checkpoint order: gate | value
+    d_x, d_w = to16(x, dtype, gpu), to16(np.ascontiguousarray(w[geglu_order(f)]), dtype, gpu)
+    out = t.full((M, f), float("nan"), dtype=t.float16 if dtype == "f16" else t.bfloat16, device=gpu)
+    linear(d_x, d_w, None, out, 4, dtype, M, 2 * f, K, 1, tile)
+    u = x.astype(np.float64) @ w.T.astype(np.float64)
+    expected = E.gelu(u[:, :f].astype(np.float32)).astype(np.float64) * u[:, f:]
+    tol = 3e-3 if dtype == "f16" else 2e-2
+    np.testing.assert_allclose(from16(out), expected, atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("tile", [-1, 2, 4, 7])
+def test_qkv_epilogue_applies_rope_to_q_and_k(gpu, tile):
+    """RoPE in fp32 before the single rounding, matching the oracle's rotate-half on the same rows."""
+    import oracle.modernbert as MB
+    t = torch()
+    rng = np.random.default_rng(23)
+    M, heads = 160, 4
+    width = heads * 64
+    x = half_round(rng.normal(0, 1, (M, width)), "f16")
+    w = half_round(rng.normal(0, 1 / math.sqrt(width), (3 * width, width)), "f16")
+    positions = np.concatenate([np.arange(96), np.arange(64)]).astype(np.int32)  # two packed sequences
+    cos, sin = MB.rope_tables(10000.0, 128)
+    q, k, vt = (t.full((heads * M * 64,), float("nan"), dtype=t.float16, device=gpu) for _ in range(3))
+    d_x, d_w, d_c, d_s, d_p = to16(x, "f16", gpu), to16(w, "f16", gpu), dev(cos, gpu), dev(sin, gpu), dev(positions, gpu)
+    check(_lib.load().laya_op_qkv(p(d_x), p(d_w), None, p(q), p(k), p(vt), p(d_c), p(d_s), p(d_p), _lib.F16, M, width,
+                                  tile, stream()))
+    sync()
+    full = (x.astype(np.float64) @ w.T.astype(np.float64)).astype(np.float32).reshape(M, 3, heads, 64)
+    cq, sq = cos[positions], sin[positions]
+    want_q = MB.rope(full[:, 0], cq, sq).transpose(1, 0, 2)
+    want_k = MB.rope(full[:, 1], cq, sq).transpose(1, 0, 2)
+    np.testing.assert_allclose(from16(q).reshape(heads, M, 64), want_q, atol=3e-3, rtol=2e-3)
+    np.testing.assert_allclose(from16(k).reshape(heads, M, 64), want_k, atol=3e-3, rtol=2e-3)
+    np.testing.assert_allclose(from16(vt).reshape(heads, 64, M), full[:, 2].transpose(1, 2, 0), atol=3e-3, rtol=2e-3)
+
+
+@pytest.mark.parametrize("mode,waves", [(0, 2), (0, 4), (0, 8), (1, 2), (1, 4)])
+@pytest.mark.parametrize("lengths", [[250, 131], [500], [1024, 333], [40]])
+def test_local_window_attention_matches_float64(gpu, lengths, mode, waves):
+    """Local layers (kernels.cu:106-107): each query sees keys with |q - k| <= 64 of its sequence;
+    blocks outside every query's window are skipped, partly masked ones masked per lane."""
+    t = torch()
+    lib = _lib.load()
+    h, window = 2, 64
+    starts = np.cumsum([0] + [span(n) for n in lengths])[:-1].astype(np.int32)
+    m = span(sum(span(n) for n in lengths) + 16)
+    x = half_round(np.random.default_rng(m + 1).normal(0, 1, (m, 3, h, 64)), "f16")
+    q = x[:, 0].transpose(1, 0, 2).copy()
+    k = x[:, 1].transpose(1, 0, 2).copy()
+    vt = x[:, 2].transpose(1, 2, 0).copy()
+    max_tiles = m // 16
+    tiles = np.zeros(4 * max_tiles, np.int32)
+    lens = np.asarray(lengths, np.int32)
+    n = lib.laya_attention_tiles(starts.ctypes.data_as(ct.POINTER(ct.c_int32)), lens.ctypes.data_as(ct.POINTER(ct.c_int32)),
+                                 len(lengths), m, lib.laya_attention_block(mode, waves),
+                                 tiles.ctypes.data_as(ct.POINTER(ct.c_int32)), max_tiles)
+    assert n > 0
+    out = t.full((m, h * 64), float("nan"), dtype=t.float16, device=gpu)
+    args = [to16(a, "f16", gpu) for a in (q, k, vt)] + [out, dev(tiles, gpu)]
+    check(lib.laya_op_attention(*[p(a) for a in args], m, h, max_tiles, mode, waves, window, _lib.F16, stream()))
+    sync()
+    got = from16(out)
+    real = np.zeros(m, bool)
+    for start, n_tok in zip(starts, lengths):
+        real[start:start + n_tok] = True
+        qq, kk, vv = x[start:start + n_tok].astype(np.float64).transpose(1, 2, 0, 3)
+        s = qq @ kk.transpose(0, 2, 1) / 8
+        idx = np.arange(n_tok)
+        s = np.where(np.abs(idx[:, None] - idx[None, :]) > window, -np.inf, s)
+        pr = np.exp(s - s.max(-1, keepdims=True))
+        pr /= pr.sum(-1, keepdims=True)
+        expected = (pr @ vv).transpose(1, 0, 2).reshape(n_tok, h * 64)
+        np.testing.assert_allclose(got[start:start + n_tok], expected, atol=6e-4, rtol=1e-3)
+    np.testing.assert_array_equal(got[~real], 0)

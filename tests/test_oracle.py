@@ -126,3 +126,53 @@ def test_planted_mistakes_fail_the_golden_check():
     w2["encoder.embeddings"] = dict(w["encoder.embeddings"], pos=np.zeros_like(w["encoder.embeddings"]["pos"]))
     assert np.abs(E.encoder_sequence(g["ids0"], w2, cfg) - g["hidden0"]).max() > 1e-2
     assert np.abs(good - g["hidden0"]).max() < 2e-5
+
+
+# ---------------- ModernBERT variant (the reference's executor) ----------------
+
+def _modernbert():
+    import oracle.modernbert as M
+    spec = synthetic.modernbert_adapter(layers=4, width=128, heads=2, intermediate=256, vocab=1000, positions=512,
+                                        max_len=512, head_layers=2)
+    g = np.load(GOLDEN / "modernbert_small.npz")
+    weights = synthetic.weights(spec, seed=int(g["seed"]), random_norms=True, std=float(g["std"]))
+    items = [(g[f"q{q}_ids"], list(g[f"q{q}_markers"]), int(g[f"q{q}_kind"])) for q in range(int(g["n_q"]))]
+    return M, spec, g, M.structured(weights, M.config(spec)), items
+
+
+def test_modernbert_encoder_matches_transformers():
+    """Pre-LN, RoPE (global and local theta), +-64 window on local layers, GeGLU, final norm."""
+    M, spec, g, w, items = _modernbert()
+    for q, (ids, _, _) in enumerate(items):
+        hidden = M.encoder_sequence(ids, w, M.config(spec))
+        np.testing.assert_allclose(hidden, g[f"q{q}_hidden"], atol=3e-5, rtol=1e-5)
+
+
+def test_modernbert_head_layers_match_torch_transformer_layers():
+    M, spec, g, w, items = _modernbert()
+    logits, acts, _ = M.forward(items, w, M.config(spec))
+    for q in range(len(items)):
+        np.testing.assert_allclose(logits[q], g[f"q{q}_logits"], atol=3e-5, rtol=1e-5)
+        np.testing.assert_allclose(acts[q], g[f"q{q}_acts"], atol=3e-5, rtol=1e-5)
+
+
+def test_modernbert_window_and_rope_are_load_bearing():
+    """A planted mistake in the oracle (no window on local layers, or RoPE off) fails the fixture."""
+    M, spec, g, w, items = _modernbert()
+    ids = items[0][0]
+    no_window = dict(M.config(spec), window=10 ** 6)
+    assert np.abs(M.encoder_sequence(ids, w, no_window) - g["q0_hidden"]).max() > 1e-3
+    same_theta = dict(M.config(spec), theta=[spec.theta[0], spec.theta[0]])
+    assert np.abs(M.encoder_sequence(ids, w, same_theta) - g["q0_hidden"]).max() > 1e-3
+
+
+def test_rope_tables_match_closed_form():
+    import oracle.modernbert as M
+    cos, sin = M.rope_tables(10000.0, 300)
+    i = np.arange(32)
+    angle = np.arange(300)[:, None] / 10000.0 ** (2 * i / 64)
+    np.testing.assert_allclose(cos, np.cos(angle), atol=2e-5)
+    np.testing.assert_allclose(sin, np.sin(angle), atol=2e-5)
+    x = np.random.default_rng(0).normal(0, 1, (300, 2, 64)).astype(np.float32)
+    r = M.rope(x, cos, sin)  # a rotation: norms per (position, pair) are preserved
+    np.testing.assert_allclose(np.hypot(r[..., :32], r[..., 32:]), np.hypot(x[..., :32], x[..., 32:]), rtol=1e-5)
