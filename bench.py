@@ -69,11 +69,6 @@ def stage_work(stage, spec, lengths):
     return None, 0.0
 
 
-def launches_per_forward(stage, spec):
-    return spec.layers if stage in ("qkv", "attention", "attn_out", "attn_norm", "ffn_up", "ffn_down",
-                                     "ffn_norm") else 1
-
-
 def progress(message):
     print(f"bench: {message}", file=sys.stderr, flush=True)
 
@@ -99,8 +94,10 @@ def stage_profile(rt, spec, sequences, questions, reps):
     lengths = [len(s) for s in sequences]
     rows = []
     for name in rt.stages():
-        ms = rt.time_stage(sequences, questions, name, 0, reps)
-        n = launches_per_forward(name, spec)
+        n, layer = rt.stage_launches(name)
+        if n == 0:
+            continue
+        ms = rt.time_stage(sequences, questions, name, layer, reps)
         bound, work = stage_work(name, spec, lengths)
         rows.append(dict(stage=name, ms=ms, launches=n, forward_ms=ms * n, bound=bound, work=work))
     return rows

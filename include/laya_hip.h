@@ -124,6 +124,10 @@ int laya_predict(void* handle, const int32_t* host_packed, const LayaShape* shap
  * afterwards. */
 int laya_stage_count(void);
 const char* laya_stage_name(int stage);
+/* How many times this engine's forward launches `stage` (0: not part of this model) and the first
+ * layer index it runs for, the `layer` argument of laya_time_stage.  Per-launch times times these
+ * counts give the per-forward breakdown of tools/profile_long.py:21-67. */
+int laya_stage_launches(void* handle, int stage, int* launches, int* first_layer);
 int laya_time_stage(void* handle, const int32_t* host_packed, const LayaShape* shape, int stage, int layer,
                     int reps, float* avg_ms);
 

@@ -324,6 +324,7 @@ constexpr TileDef kTiles[] = {
     {256, 256, 2, 4, 1},  // 7: 8 waves of 128x64, large M
     {256, 128, 4, 2, 1},  // 8: 8 waves of 64x64
     {128, 256, 2, 4, 1},  // 9: 8 waves of 64x64
+    {128, 64, 4, 1, 3},   // 10: wave 32x64, whole heads per wave for RoPE when N is not a multiple of 128
 };
 constexpr int kTileCount = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -347,6 +348,7 @@ hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
     LAYA_TILE(7, 256, 256, 2, 4, 1)
     LAYA_TILE(8, 256, 128, 4, 2, 1)
     LAYA_TILE(9, 128, 256, 2, 4, 1)
+    LAYA_TILE(10, 128, 64, 4, 1, 3)
 #undef LAYA_TILE
     default: return hipErrorInvalidValue;
   }
@@ -398,8 +400,10 @@ void gemm_plan(int M, int N, int K, Epi epi, int cus, int* tile, int* splits, bo
   // and, for the fp32 (split-K capable) epilogue, to K splits until the grid covers the chip.
   // Eight-wave tiles first: with two waves per SIMD they sustain the most MFMA throughput when
   // the grid is large enough; then four-wave tiles from large to small.
+  // Tile 10 is only the RoPE fallback for N not a multiple of 128 (odd head counts): every other
+  // RoPE-capable tile is 128 or more columns wide.
   const int order[] = {7, 9, 8, 0, 1, 2, 3, 4, 5, 6};
-  int best = rope ? 4 : 5, best_split = 1;
+  int best = rope ? (N % 128 ? 10 : 4) : 5, best_split = 1;
   for (int id : order) {
     const TileDef& d = kTiles[id];
     if (N % d.bn) continue;

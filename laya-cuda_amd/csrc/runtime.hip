@@ -1076,6 +1076,23 @@ int laya_stage_count(void) { return kStageCount; }
 
 const char* laya_stage_name(int stage) { return stage >= 0 && stage < kStageCount ? kStageNames[stage] : nullptr; }
 
+int laya_stage_launches(void* handle, int stage, int* launches, int* first_layer) {
+  Engine* E = static_cast<Engine*>(handle);
+  if (!E) return fail(nullptr, Failure{LAYA_EINVAL, "null handle"});
+  return guarded(E, [&] {
+    LAYA_REQUIRE(launches && first_layer, "null output");
+    LAYA_REQUIRE(stage >= 0 && stage < kStageCount, "unknown stage");
+    const int span = per_layer(stage) ? E->cfg.layers : per_head_layer(stage) ? E->cfg.head_layers : 1;
+    *launches = 0;
+    *first_layer = -1;
+    for (int j = 0; j < span; ++j)
+      if (stage_used(*E, stage, j)) {
+        if (*launches == 0) *first_layer = j;
+        ++*launches;
+      }
+  });
+}
+
 int laya_time_stage(void* handle, const int32_t* host_packed, const LayaShape* shape, int stage, int layer, int reps,
                     float* avg_ms) {
   Engine* E = static_cast<Engine*>(handle);

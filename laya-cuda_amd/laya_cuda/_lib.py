@@ -45,6 +45,7 @@ SIGNATURES = {
     "laya_stage_count": ([], _i),
     "laya_stage_name": ([_i], ct.c_char_p),
     "laya_time_stage": ([_p, _ip, ct.POINTER(LayaShape), _i, _i, _i, _fp], _i),
+    "laya_stage_launches": ([_p, _i, ct.POINTER(ct.c_int32), ct.POINTER(ct.c_int32)], _i),
     "laya_read_weight": ([_p, ct.c_char_p, _fp, _i64], _i),
     "laya_used_bytes": ([_p], _i64),
     "laya_slot_count": ([_p], _i),

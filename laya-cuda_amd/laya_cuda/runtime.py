@@ -232,6 +232,15 @@ class Runtime:
         lib = _lib.load()
         return [lib.laya_stage_name(i).decode() for i in range(lib.laya_stage_count())]
 
+    def stage_launches(self, stage):
+        """(launches per forward, first layer) of ``stage`` in this model; (0, -1) if it has none."""
+        if self._handle is None:
+            raise RuntimeError("Runtime is closed")
+        index = self.stages().index(stage) if isinstance(stage, str) else int(stage)
+        n, first = ct.c_int32(), ct.c_int32()
+        _lib.check(_lib.load().laya_stage_launches(self._handle, index, ct.byref(n), ct.byref(first)), self._handle)
+        return int(n.value), int(first.value)
+
     def time_stage(self, sequences, questions, stage, layer=0, reps=50, key=None):
         """Average device time (ms) of one launch of ``stage`` on this request's shape slot,
         measured with events around ``reps`` back-to-back launches on the engine's stream."""

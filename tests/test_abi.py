@@ -117,3 +117,12 @@ def test_create_rejects_unbuilt_variants_before_touching_the_device():
     cfg.heads = 2  # width != heads * 64
     assert lib.laya_create(ct.byref(cfg), 0, 4, ct.byref(handle)) == _lib.EINVAL
     assert "64-wide" in _lib.error(None)
+
+
+def test_stage_queries_without_a_handle():
+    lib = _lib.load()
+    names = [lib.laya_stage_name(i).decode() for i in range(lib.laya_stage_count())]
+    assert names[0] == "embed_norm" and "attention" in names and "head_qkv" in names
+    assert lib.laya_stage_name(len(names)) is None
+    n, first = ct.c_int32(), ct.c_int32()
+    assert lib.laya_stage_launches(None, 0, ct.byref(n), ct.byref(first)) == _lib.EINVAL

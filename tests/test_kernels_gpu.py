@@ -165,7 +165,7 @@ def linear(x, w, bias, out, kind, dtype, M, N, K, splits, tile):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("tile", range(10))
+@pytest.mark.parametrize("tile", range(11))
 def test_linear_tiles_match_fp32_product(gpu, dtype, tile):
     t = torch()
     rng = np.random.default_rng(tile)
@@ -343,13 +343,14 @@ def test_linear_geglu_epilogue_on_interleaved_rows(gpu, dtype, tile):
     np.testing.assert_allclose(from16(out), expected, atol=tol, rtol=tol)
 
 
-@pytest.mark.parametrize("tile", [-1, 2, 4, 7])
-def test_qkv_epilogue_applies_rope_to_q_and_k(gpu, tile):
-    """RoPE in fp32 before the single rounding, matching the oracle's rotate-half on the same rows."""
+@pytest.mark.parametrize("tile,heads", [(-1, 4), (2, 4), (4, 4), (7, 4), (10, 4), (-1, 3), (10, 3), (-1, 1)])
+def test_qkv_epilogue_applies_rope_to_q_and_k(gpu, tile, heads):
+    """RoPE in fp32 before the single rounding, matching the oracle's rotate-half on the same rows;
+    odd head counts (3 * width not a multiple of 128) take the 128x64 tile."""
     import oracle.modernbert as MB
     t = torch()
     rng = np.random.default_rng(23)
-    M, heads = 160, 4
+    M = 160
     width = heads * 64
     x = half_round(rng.normal(0, 1, (M, width)), "f16")
     w = half_round(rng.normal(0, 1 / math.sqrt(width), (3 * width, width)), "f16")

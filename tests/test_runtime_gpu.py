@@ -283,3 +283,31 @@ def test_modernbert_rejects_mixed_types_on_a_shared_sequence(gpu):
             rt.predict_sequences([[1, 2, 3, 4]], [(0, [1], 0), (0, [2], 1)])
     finally:
         rt.close()
+
+
+def test_stage_launch_counts_follow_the_variant(gpu):
+    """Per-forward launch counts: encoder stages once per layer, head-layer stages once per head
+    layer (the row gather only before the last), variant-only stages zero elsewhere."""
+    bert = synthetic.adapter(None, layers=3, width=64, heads=1, intermediate=256, vocab=100, positions=64,
+                             max_len=64)
+    rt = Runtime(bert, 0, 1, weights=synthetic.weights(bert, seed=1))
+    try:
+        counts = {name: rt.stage_launches(name) for name in rt.stages()}
+        assert counts["embed_norm"] == (1, 0) and counts["qkv"] == (3, 0) and counts["ffn_norm"] == (3, 0)
+        assert counts["head_gather"] == (1, 0) and counts["act_out"] == (1, 0)
+        assert counts["type_norm"] == (0, -1) and counts["head_qkv"] == (0, -1)
+    finally:
+        rt.close()
+    modern = synthetic.modernbert_adapter(layers=2, width=64, heads=1, intermediate=128, vocab=100, positions=128,
+                                          max_len=64, head_layers=3)
+    rt = Runtime(modern, 0, 1, weights=synthetic.weights(modern, seed=1))
+    try:
+        counts = {name: rt.stage_launches(name) for name in rt.stages()}
+        assert counts["qkv"] == (2, 0) and counts["type_norm"] == (1, 0) and counts["head_qkv"] == (3, 0)
+        assert counts["head_gather_rows"] == (1, 2) and counts["head_gather"] == (0, -1)
+        items = [(list(range(5, 45)), [3, 7], 1)]
+        for name, (n, layer) in counts.items():
+            if n:
+                assert rt.time_stage([items[0][0]], [(0, items[0][1], 1)], name, layer, reps=2) > 0
+    finally:
+        rt.close()
