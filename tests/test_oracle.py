@@ -176,3 +176,16 @@ def test_rope_tables_match_closed_form():
     x = np.random.default_rng(0).normal(0, 1, (300, 2, 64)).astype(np.float32)
     r = M.rope(x, cos, sin)  # a rotation: norms per (position, pair) are preserved
     np.testing.assert_allclose(np.hypot(r[..., :32], r[..., 32:]), np.hypot(x[..., :32], x[..., 32:]), rtol=1e-5)
+
+
+def test_rope_scores_depend_only_on_relative_position():
+    """q.k after RoPE at positions (i, j) equals the same vectors' score at (i + s, j + s)."""
+    import oracle.modernbert as M
+    cos, sin = M.rope_tables(160000.0, 400)
+    rng = np.random.default_rng(1)
+    q, k = rng.normal(0, 1, (2, 1, 1, 64)).astype(np.float32)
+    def score(i, j):
+        return float((M.rope(q, cos[i:i + 1], sin[i:i + 1]) * M.rope(k, cos[j:j + 1], sin[j:j + 1])).sum())
+    for i, j, s in [(0, 5, 7), (10, 3, 200), (64, 64, 300), (1, 129, 100)]:
+        assert abs(score(i, j) - score(i + s, j + s)) < 2e-4 * max(1.0, abs(score(i, j)))
+    assert abs(score(0, 5) - score(0, 6)) > 1e-4  # and it does depend on the offset
