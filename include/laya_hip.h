@@ -184,7 +184,7 @@ int laya_op_linear(const void* x, const void* w, const float* bias, void* out, i
 /* QKV projection with the head-major epilogue that replaces `layout` (kernels.cu:68-82):
  * q, k [heads][M][64], vt [heads][64][M].  With rope_cos non-NULL, Q and K are rotated (rotate-half
  * RoPE, kernels.cu:73-77) in fp32 before rounding, by the [positions][32] cos/sin tables at each
- * row's positions[row]. */
+ * row's positions[row].  M must be a multiple of 8. */
 int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* k, void* vt,
                 const float* rope_cos, const float* rope_sin, const int32_t* positions, int dtype16,
                 int M, int width, int tile, void* stream);

@@ -22,6 +22,8 @@
 //          (replaces the reference's separate `layout` pass, kernels.cu:68-82).
 #include "kernels.hpp"
 
+#include <type_traits>
+
 namespace laya {
 
 namespace {
@@ -134,59 +136,118 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
       early_bias[r4] = with_bias ? *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + 8 * r4 + 4 * kg)
                                  : make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  // One 64-deep slab from LDS buffer `buf`: four 16-deep MFMA steps.  With at most 8 MFMA tiles per
+  // wave the fragments are double-buffered in registers, so the LDS reads of step kk+1 are in
+  // flight while the MFMAs of step kk run; larger wave tiles have no registers to spare for that.
+  constexpr bool kFrag2 = TM * TN <= 8;
   auto compute = [&](int buf) {
     const T* cA = sA + buf * BM * BK;
     const T* cB = sB + buf * BN * BK;
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
+    T8 af[kFrag2 ? 2 : 1][TM], bfr[kFrag2 ? 2 : 1][TN];
+    auto fetch = [&](int kk, int s) {
       const int ch = kk * 2 + kg;
-      T8 af[TM], bfr[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = wm0 + i * 32 + lrow;
-        af[i] = *reinterpret_cast<const T8*>(cA + r * BK + ((ch ^ (r & 7)) << 3));
+        af[s][i] = *reinterpret_cast<const T8*>(cA + r * BK + ((ch ^ (r & 7)) << 3));
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int r = wn0 + j * 32 + lrow;
-        bfr[j] = *reinterpret_cast<const T8*>(cB + r * BK + ((ch ^ (r & 7)) << 3));
+        bfr[s][j] = *reinterpret_cast<const T8*>(cB + r * BK + ((ch ^ (r & 7)) << 3));
+      }
+    };
+    if constexpr (kFrag2) fetch(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int s = kFrag2 ? (kk & 1) : 0;
+      if constexpr (kFrag2) {
+        if (kk + 1 < BK / 16) fetch(kk + 1, (kk + 1) & 1);
+      } else {
+        fetch(kk, 0);
       }
       // Weights as the MFMA A operand: the accumulator holds C^T, so each lane ends with four
-      // consecutive output columns of one row (vector stores in the epilogue).
+      // consecutive output columns of one row.
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(bfr[j], af[i], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(bfr[s][j], af[s][i], acc[i][j]);
     }
   };
 
-  // Pipeline: slab s >= 1 travels in register set (s-1) % PF, issued PF slabs ahead of its use, so
-  // PF slabs of global loads are in flight while the MFMAs consume the slab in LDS.  Two LDS
-  // buffers; one barrier per slab.  Every step issues its loads unconditionally (slab indices past
-  // the end are clamped to the last slab and never used), so the number of loads in flight is the
-  // same on every path and the compiler's wait counts keep the PF-1 younger sets in flight.
   const int n = ke - kb;
-  if (n > 0) {
-    i32x4 ra[PF][ACH], rb[PF][BCH];
-    auto step = [&](int it, int u) {
-      compute(it & 1);
-      lstore((it + 1) & 1, ra[u], rb[u]);  // at it = n-1 this fills the idle buffer; never read
-      gload(kb + min(it + 1 + PF, n - 1), ra[u], rb[u]);
-      __syncthreads();
+  if constexpr (PF == 1) {
+    // Large tiles: slabs go from global memory straight into LDS (global_load_lds_dwordx4: no
+    // register staging, no LDS store instructions).  Slab it+1 is loaded into the other buffer
+    // while slab it feeds the MFMAs; each wave waits for its own loads, then one barrier makes the
+    // slab visible to all.  A load instruction fills 1 KB of LDS = 8 rows of 128 B, lane l at row
+    // l/8, physical 16-byte chunk l%8, so lane l fetches logical chunk (l%8) ^ (l/8): the same
+    // XOR-swizzled layout as the register path.
+    typedef __attribute__((address_space(3))) void* LdsPtr;
+    typedef __attribute__((address_space(1))) void* GlobalPtr;
+    constexpr int NW = WM * WN;
+    constexpr int AG = BM / 8 / NW, BG = BN / 8 / NW;  // 8-row groups per wave per slab
+    static_assert(AG * 8 * NW == BM && BG * 8 * NW == BN, "whole 8-row groups per wave");
+    const int lr = lane >> 3, lch = (lane & 7) ^ lr;
+    auto dload = [&](int kt, int buf) {
+      const int k0 = kt * BK + lch * 8;
+#pragma unroll
+      for (int i = 0; i < AG; ++i) {
+        const int grp = wave + NW * i;
+        const int g = min(m0 + grp * 8 + lr, a.M - 1);  // rows past M read row M-1, never stored
+        __builtin_amdgcn_global_load_lds((GlobalPtr)(A + static_cast<size_t>(g) * a.lda + k0),
+                                         (LdsPtr)(sA + buf * BM * BK + grp * 8 * BK), 16, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < BG; ++i) {
+        const int grp = wave + NW * i;
+        __builtin_amdgcn_global_load_lds((GlobalPtr)(B + static_cast<size_t>(n0 + grp * 8 + lr) * a.ldb + k0),
+                                         (LdsPtr)(sB + buf * BN * BK + grp * 8 * BK), 16, 0, 0);
+      }
     };
-    gload(kb, ra[0], rb[0]);
-    lstore(0, ra[0], rb[0]);
-#pragma unroll
-    for (int p = 0; p < PF; ++p) gload(kb + min(1 + p, n - 1), ra[p], rb[p]);
-    __syncthreads();
-    int it = 0;
-    for (; it + PF <= n; it += PF) {
-#pragma unroll
-      for (int u = 0; u < PF; ++u) step(it + u, u);
+    // s_waitcnt immediate for vmcnt(0) with expcnt and lgkmcnt left free (gfx9 field layout).
+    constexpr int kVmcnt0 = 0x0F70;
+    if (n > 0) {
+      dload(kb, 0);
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      __syncthreads();
+      for (int it = 0; it < n; ++it) {
+        if (it + 1 < n) dload(kb + it + 1, (it + 1) & 1);
+        compute(it & 1);
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+        __syncthreads();
+      }
     }
+  } else {
+    // Small tiles (batch-1 problems): slab s >= 1 travels in register set (s-1) % PF, issued PF
+    // slabs ahead of its use, so PF slabs of global loads are in flight while the MFMAs consume the
+    // slab in LDS.  Two LDS buffers; one barrier per slab.  Every step issues its loads
+    // unconditionally (slab indices past the end are clamped to the last slab and never used), so
+    // the number of loads in flight is the same on every path and the compiler's wait counts keep
+    // the PF-1 younger sets in flight.
+    if (n > 0) {
+      i32x4 ra[PF][ACH], rb[PF][BCH];
+      auto step = [&](int it, int u) {
+        compute(it & 1);
+        lstore((it + 1) & 1, ra[u], rb[u]);  // at it = n-1 this fills the idle buffer; never read
+        gload(kb + min(it + 1 + PF, n - 1), ra[u], rb[u]);
+        __syncthreads();
+      };
+      gload(kb, ra[0], rb[0]);
+      lstore(0, ra[0], rb[0]);
 #pragma unroll
-    for (int u = 0; u < PF; ++u)
-      if (it + u < n) step(it + u, u);
+      for (int p = 0; p < PF; ++p) gload(kb + min(1 + p, n - 1), ra[p], rb[p]);
+      __syncthreads();
+      int it = 0;
+      for (; it + PF <= n; it += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) step(it + u, u);
+      }
+#pragma unroll
+      for (int u = 0; u < PF; ++u)
+        if (it + u < n) step(it + u, u);
+    }
+    __syncthreads();  // the epilogue reuses LDS
   }
 
   // Epilogue.  Element r of lane l in a 32x32 tile of C^T is output column 8*(r/4) + 4*(l/32) +
@@ -204,62 +265,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
     }
   };
   typedef typename Vec4<T>::type T4;
+  if constexpr (E == Epi::GEGLU) {
+    // Weight rows interleaved in 32-row groups (16 gate rows, then their 16 value rows), so a lane
+    // holds gate column c (r4 < 2) and its value column c + 16 (r4 + 2): out[f] = gelu(gate) *
+    // value, 16 features per 32 columns (the reference's activate mode 2).
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int row = m0 + wm0 + i * 32 + lrow;
-    if (row >= a.M) continue;
-    if constexpr (E == Epi::QKV) {
-      if (a.rope_cos) {
-        // RoPE on Q and K (rotate-half, the reference's `layout`, kernels.cu:73-77) on the fp32
-        // accumulator before the single rounding: tiles j and j+1 hold dims d and d+32 of one head.
-        const int pos = a.positions[row];
-        const float* cs = a.rope_cos + static_cast<size_t>(pos) * 32;
-        const float* sn = a.rope_sin + static_cast<size_t>(pos) * 32;
+    for (int i = 0; i < TM; ++i) {
+      const int row = m0 + wm0 + i * 32 + lrow;
+      if (row >= a.M) continue;
 #pragma unroll
-        for (int j = 0; j + 1 < TN; j += 2) {
-          const int col = n0 + wn0 + j * 32;
-          const int part = col / a.width, hn = col - part * a.width, head = hn >> 6;
-#pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) {
-            const int dim = 8 * r4 + 4 * kg;
-            T4 lo, hi;
-            float v0[4], v1[4];
-            take(i, j, r4, v0);
-            take(i, j + 1, r4, v1);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              float x0 = v0[e], x1 = v1[e];
-              if (part < 2) {
-                const float c = cs[dim + e], sv = sn[dim + e];
-                const float y0 = x0 * c - x1 * sv, y1 = x1 * c + x0 * sv;
-                x0 = y0;
-                x1 = y1;
-              }
-              lo[e] = to_half<T>(x0);
-              hi[e] = to_half<T>(x1);
-            }
-            if (part < 2) {
-              T* dst = static_cast<T*>(part == 0 ? a.q : a.k) + (static_cast<size_t>(head) * a.M + row) * 64 + dim;
-              *reinterpret_cast<T4*>(dst) = lo;
-              *reinterpret_cast<T4*>(dst + 32) = hi;
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                static_cast<T*>(a.vt)[(static_cast<size_t>(head) * 64 + dim + e) * a.M + row] = lo[e];
-                static_cast<T*>(a.vt)[(static_cast<size_t>(head) * 64 + 32 + dim + e) * a.M + row] = hi[e];
-              }
-            }
-          }
-        }
-        continue;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      if constexpr (E == Epi::GEGLU) {
-        // Weight rows interleaved in 32-row groups (16 gate rows, then their 16 value rows), so a
-        // lane holds gate column c (r4 < 2) and its value column c + 16 (r4 + 2):
-        // out[f] = gelu(gate) * value, 16 features per 32 columns (the reference's activate mode 2).
+      for (int j = 0; j < TN; ++j) {
         const int fbase = ((n0 + wn0 + j * 32) >> 1) + 4 * kg;
 #pragma unroll
         for (int r4 = 0; r4 < 2; ++r4) {
@@ -271,38 +286,148 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
           for (int e = 0; e < 4; ++e) h[e] = to_half<T>(gelu16(gate[e]) * value[e]);
           *reinterpret_cast<T4*>(static_cast<T*>(a.out) + static_cast<long long>(row) * a.ldo + fbase + 8 * r4) = h;
         }
-        continue;
+      }
+    }
+    return;
+  }
+
+  // Every other epilogue leaves through LDS, one 32x32 tile at a time in this wave's own region
+  // (the main loop's buffers are free: its last barrier has passed): the lanes write their column
+  // quads, then read back 16-byte chunks of whole row segments, so each store instruction covers
+  // 16 rows x 64 B (16-bit) or 8 rows x 128 B (fp32) instead of 32 rows x 8-16 B.  V^T goes through
+  // a transposed stage, so its stores are runs of 8 consecutive tokens.  A wave's LDS accesses
+  // execute in issue order, so the region needs no barrier between writes and reads.
+  constexpr int SP = E == Epi::F32 ? 36 : 40;  // stage pitch in elements: 144 B / 80 B, 16-byte aligned
+  typedef typename std::conditional<E == Epi::F32, float, T>::type S;
+  static_assert(static_cast<size_t>(WM * WN) * 32 * SP * sizeof(S) <= static_cast<size_t>(2) * (BM + BN) * BK * 2,
+                "the staging regions fit in the main loop's LDS");
+  S* stg = reinterpret_cast<S*>(smem_raw) + wave * 32 * SP;
+  const int rbase = m0 + wm0;  // first output row of this wave
+  // Row-major 32x32 tile: lane values h[r4] = columns 8 r4 + 4 kg .. +3 of tile row lrow; chunk
+  // (r, c) (tile row r, first column c) is stored at dst(row, c) when row = rbase + 32 i + r < M.
+  auto emit_rows = [&](int i, const auto (&h)[4], auto dst) {
+    typedef typename std::remove_cv<typename std::remove_reference<decltype(h[0])>::type>::type Q;
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) *reinterpret_cast<Q*>(stg + lrow * SP + 8 * r4 + 4 * kg) = h[r4];
+    constexpr int EPC = 16 / sizeof(S), CPR = 32 / EPC;  // elements per chunk, chunks per row
+#pragma unroll
+    for (int t = 0; t < 32 * CPR / 64; ++t) {
+      const int c = lane + 64 * t, r = c / CPR, col = (c % CPR) * EPC;
+      const i32x4 v = *reinterpret_cast<const i32x4*>(stg + r * SP + col);
+      const int row = rbase + i * 32 + r;
+      if (row < a.M) *reinterpret_cast<i32x4*>(dst(row, col)) = v;
+    }
+  };
+
+  if constexpr (E == Epi::F32) {
+    float* out = static_cast<float*>(a.out) + z * a.split_stride;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        float4 h[4];
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          float v[4];
+          take(i, j, r4, v);
+          h[r4] = make_float4(v[0], v[1], v[2], v[3]);
+        }
+        const int col0 = n0 + wn0 + j * 32;
+        emit_rows(i, h, [&](int row, int col) { return out + static_cast<long long>(row) * a.ldo + col0 + col; });
+      }
+  } else if constexpr (E == Epi::QKV) {
+    T* const vt = static_cast<T*>(a.vt);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int row_lane = rbase + i * 32 + lrow;
+      // RoPE on Q and K (rotate-half, the reference's `layout`, kernels.cu:73-77) on the fp32
+      // accumulator before the single rounding: tiles j and j+1 hold dims d and d+32 of one head.
+      const float* cs = nullptr;
+      const float* sn = nullptr;
+      if (a.rope_cos) {
+        const int pos = a.positions[min(row_lane, a.M - 1)];
+        cs = a.rope_cos + static_cast<size_t>(pos) * 32;
+        sn = a.rope_sin + static_cast<size_t>(pos) * 32;
       }
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const int col = n0 + wn0 + j * 32 + 8 * r4 + 4 * kg;
-        float v[4];
-        take(i, j, r4, v);
-        if constexpr (E == Epi::F32) {
-          *reinterpret_cast<float4*>(static_cast<float*>(a.out) + z * a.split_stride +
-                                     static_cast<long long>(row) * a.ldo + col) = make_float4(v[0], v[1], v[2], v[3]);
-        } else if constexpr (E == Epi::QKV) {
-          const int part = col / a.width, hn = col - part * a.width, head = hn >> 6, dim = hn & 63;
-          T4 h;
+      for (int j = 0; j < TN; ++j) {
+        const int col0 = n0 + wn0 + j * 32;
+        const int part = col0 / a.width, hn = col0 - part * a.width, head = hn >> 6, dim0 = hn & 63;
+        if (part < 2) {
+          T* const qk = static_cast<T*>(part == 0 ? a.q : a.k) + static_cast<size_t>(head) * a.M * 64;
+          auto qdst = [&](int d0) {
+            return [=](int row, int col) { return qk + static_cast<size_t>(row) * 64 + d0 + col; };
+          };
+          if (cs) {
+            if (j & 1) continue;  // emitted with its pair
+            if constexpr (TN >= 2) {
+              T4 lo[4], hi[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = to_half<T>(v[e]);
-          if (part < 2) {
-            T* dst = static_cast<T*>(part == 0 ? a.q : a.k);
-            *reinterpret_cast<T4*>(dst + (static_cast<size_t>(head) * a.M + row) * 64 + dim) = h;
-          } else {
+              for (int r4 = 0; r4 < 4; ++r4) {
+                const int dim = 8 * r4 + 4 * kg;
+                float v0[4], v1[4];
+                take(i, j, r4, v0);
+                take(i, j + 1, r4, v1);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              static_cast<T*>(a.vt)[(static_cast<size_t>(head) * 64 + dim + e) * a.M + row] = h[e];
+                for (int e = 0; e < 4; ++e) {
+                  const float c = cs[dim + e], sv = sn[dim + e];
+                  lo[r4][e] = to_half<T>(v0[e] * c - v1[e] * sv);
+                  hi[r4][e] = to_half<T>(v1[e] * c + v0[e] * sv);
+                }
+              }
+              emit_rows(i, lo, qdst(0));
+              emit_rows(i, hi, qdst(32));
+            }
+            continue;
           }
-        } else {
-          T4 h;
+          T4 h[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            h[e] = to_half<T>(E == Epi::GELU ? gelu16(v[e]) : E == Epi::RELU ? fmaxf(v[e], 0.f) : v[e]);
-          *reinterpret_cast<T4*>(static_cast<T*>(a.out) + static_cast<long long>(row) * a.ldo + col) = h;
+          for (int r4 = 0; r4 < 4; ++r4) {
+            float v[4];
+            take(i, j, r4, v);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) h[r4][e] = to_half<T>(v[e]);
+          }
+          emit_rows(i, h, qdst(dim0));
+        } else {
+          // V^T [head][64][M]: stage transposed (tile column = head dim as the LDS row, 32 tokens
+          // per row), then store runs of 8 tokens; M is a multiple of 8, so a run is all in or out.
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            float v[4];
+            take(i, j, r4, v);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) stg[(8 * r4 + 4 * kg + e) * SP + lrow] = to_half<T>(v[e]);
+          }
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int c = lane + 64 * t, d = c >> 2, tok = (c & 3) * 8;
+            const i32x4 v = *reinterpret_cast<const i32x4*>(stg + d * SP + tok);
+            const int row = rbase + i * 32 + tok;
+            if (row < a.M)
+              *reinterpret_cast<i32x4*>(vt + (static_cast<size_t>(head) * 64 + dim0 + d) * a.M + row) = v;
+          }
         }
       }
     }
+  } else {
+    T* out = static_cast<T*>(a.out);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        T4 h[4];
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          float v[4];
+          take(i, j, r4, v);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            h[r4][e] = to_half<T>(E == Epi::GELU ? gelu16(v[e]) : E == Epi::RELU ? fmaxf(v[e], 0.f) : v[e]);
+        }
+        const int col0 = n0 + wn0 + j * 32;
+        emit_rows(i, h, [&](int row, int col) { return out + static_cast<long long>(row) * a.ldo + col0 + col; });
+      }
   }
 }
 
@@ -438,6 +563,7 @@ hipError_t launch_gemm(const GemmArgs& args, Epi epi, DType t, int tile, hipStre
   // RoPE needs both halves of a head in one lane: wave tiles of 64-column multiples.
   const TileDef& td = kTiles[tile];
   if (epi == Epi::QKV && a.rope_cos && (td.bn / td.wn) % 64) return hipErrorInvalidValue;
+  if (epi == Epi::QKV && a.M % 8) return hipErrorInvalidValue;  // V^T is stored in runs of 8 tokens
   if (epi == Epi::GEGLU && (a.N % 32 || a.ldo * 2 < a.N)) return hipErrorInvalidValue;
   if (epi == Epi::F32 && a.splits != 1 && a.bias) return hipErrorInvalidValue;  // bias joins the sum later
   const bool h = t == DType::F16;

@@ -1238,6 +1238,7 @@ int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* 
     if (tile < 0) gemm_plan(M, 3 * width, width, Epi::QKV, 256, &tile, &splits, rope);
     LAYA_REQUIRE(tile < gemm_tile_count(), "bad tile id");
     LAYA_REQUIRE(width % 64 == 0 && (3 * width) % gemm_tile(tile).bn == 0, "width does not fit the tile");
+    LAYA_REQUIRE(M % 8 == 0, "rows must be a multiple of 8 (V^T is stored in runs of 8 tokens)");
     GemmArgs g{};
     g.a = x; g.b = w; g.M = M; g.N = 3 * width; g.K = width; g.lda = width; g.ldb = width; g.bias = bias;
     g.splits = 1; g.q = q; g.k = k; g.vt = vt; g.width = width;
