@@ -249,6 +249,85 @@ def run_extras(args):
     return extras
 
 
+def _drive(submit, work, concurrency, samples, warmup):
+    """Keep ``concurrency`` requests outstanding until ``samples`` complete; per-request latency is
+    taken at completion (a done-callback), not when the driver polls (tools/benchmark_batching.py
+    protocol of the reference)."""
+    from concurrent.futures import FIRST_COMPLETED, Future, wait
+    for i in range(0, warmup, concurrency):
+        for f in [submit(*work[j % len(work)]) for j in range(i, min(i + concurrency, warmup))]:
+            f.result()
+    pending, latencies, sent = {}, [], 0
+    start = time.perf_counter()
+    while sent < samples or pending:
+        while sent < samples and len(pending) < concurrency:
+            before = time.perf_counter()
+            original, done = submit(*work[sent % len(work)]), Future()
+
+            def complete(f, finished=done):
+                try:
+                    f.result()
+                    finished.set_result(time.perf_counter())
+                except BaseException as error:  # reported by the driver
+                    finished.set_exception(error)
+            original.add_done_callback(complete)
+            pending[done] = before
+            sent += 1
+        finished, _ = wait(pending, return_when=FIRST_COMPLETED)
+        for f in finished:
+            latencies.append((f.result() - pending.pop(f)) * 1e3)
+    seconds = time.perf_counter() - start
+    return {"p50_ms": round(pct(latencies, 50), 3), "p95_ms": round(pct(latencies, 95), 3),
+            "p99_ms": round(pct(latencies, 99), 3), "requests_s": round(samples / seconds, 1)}
+
+
+def run_batching(args):
+    """Serialized Engine vs BatchEngine under bounded outstanding load on the 12-layer d=768 encoder
+    (tools/benchmark_batching.py of the reference): one 2-option question per request, short
+    (32-token), long (1,024-token) and alternating cases, 1 / 8 / 32 requests outstanding."""
+    import shutil
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+
+    from laya_cuda import BatchEngine, Engine, synthetic
+    spec = synthetic.WORKLOADS["ragged32"]
+    config = synthetic.encoder_config(spec["layers"], spec["width"], spec["heads"], spec["intermediate"],
+                                      spec["vocab"], spec["positions"])
+    task = dict(synthetic.task_config(spec["max_len"]), head_max_len=64)
+    root = tempfile.mkdtemp(prefix="laya_batching_")
+    out = {"model": "12L/768 post-LN encoder, fp16 operands, max_len 1024", "samples": args.batching_samples,
+           "batch_tokens": 4096, "cases": {}}
+    try:
+        path = synthetic.checkpoint(root, config, task, seed=0, random_norms=False)[0]
+        questions = {"0": {"type": "choice", "instructions": "Choose a topic.", "criteria": ["payment", "software"]}}
+        probe = Engine(str(path), max_cached_shapes=2)
+        overhead = len(probe.adapter.prepare("", questions)[0][0])
+        probe.close()
+        short = (" refund" * max(0, 32 - overhead), questions)
+        long = (" refund" * max(0, spec["max_len"] - overhead), questions)
+        cases = {"short": [short], "long": [long], "mixed": [short, long]}
+        for mode in ("serial", "batch"):
+            executor = ThreadPoolExecutor(1) if mode == "serial" else None
+            engine = (executor.submit(Engine, str(path)).result() if executor
+                      else BatchEngine(str(path), max_batch_tokens=4096))
+            submit = ((lambda st, q: executor.submit(engine.predict, st, q)) if executor else engine.submit)
+            try:
+                for case, work in cases.items():
+                    for concurrency in (1, 8, 32):
+                        r = _drive(submit, work, concurrency, args.batching_samples, 20)
+                        out["cases"].setdefault(case, {}).setdefault(mode, {})[str(concurrency)] = r
+                        progress(f"batching {case} {mode} x{concurrency}: p50 {r['p50_ms']} ms, {r['requests_s']} req/s")
+            finally:
+                if executor:
+                    executor.submit(engine.close).result()
+                    executor.shutdown()
+                else:
+                    engine.close()
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+    return out
+
+
 def _sync():
     try:
         import torch
@@ -268,6 +347,9 @@ def main():
     ap.add_argument("--extras", action="store_true")
     ap.add_argument("--eager", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--batching", action="store_true",
+                    help="with --extras: serialized Engine vs BatchEngine under 1/8/32 outstanding requests")
+    ap.add_argument("--batching-samples", type=int, default=100)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the encoder path shards by request with no collective, and "
@@ -276,6 +358,8 @@ def main():
     line = run_headline(args)
     if args.extras:
         line["extras"] = run_extras(args)
+        if args.batching:
+            line["extras"]["batching"] = run_batching(args)
     print(json.dumps(line), flush=True)
 
 

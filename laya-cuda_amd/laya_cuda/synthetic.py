@@ -150,3 +150,53 @@ def valid_flops(spec, lengths):
     8 L d^2 + 4 L d f + 4 L^2 d (QKV 6Ld^2, out 2Ld^2, FFN 4Ldf, QK^T + PV 4L^2 d)."""
     d, f = spec.width, spec.intermediate
     return sum(spec.layers * (8 * L * d * d + 4 * L * d * f + 4 * L * L * d) for L in lengths)
+
+
+# A small fixed corpus for the checkpoint tokenizer: support-ticket vocabulary plus the question
+# scaffolding ("<type> question: ...", the noul defaults, score levels) that prepare() encodes.
+TOKENIZER_CORPUS = [
+    "refund the payment for the order", "choose a team for billing questions", "choose a topic",
+    "the customer asks about a late delivery and wants a refund", "yes, the statement holds",
+    "no, the statement does not hold", "level 0: not urgent", "level 1: urgent", "level 2: critical",
+    "billing team handles invoices and payment errors", "shipping team handles delivery and tracking",
+    "software questions go to the engineering queue", "other questions go to the general support queue",
+    "noul question: is the customer angry?", "choice question: route the ticket",
+    "score question: how urgent is the ticket?", "payment software ticket order customer delivery",
+]
+TOKENIZER_SPECIALS = ["[PAD]", "[UNK]", "[CLS]", "[SEP]", "[MASK]"]
+
+
+def tokenizer(vocab_size=400):
+    """Byte-pair tokenizer trained offline on TOKENIZER_CORPUS (whitespace pre-tokenizer; ids 0-4 are
+    [PAD] [UNK] [CLS] [SEP] [MASK])."""
+    from tokenizers import Tokenizer, models, pre_tokenizers, trainers
+    tok = Tokenizer(models.BPE(unk_token="[UNK]"))
+    tok.pre_tokenizer = pre_tokenizers.Whitespace()
+    tok.train_from_iterator(TOKENIZER_CORPUS * 10, trainers.BpeTrainer(vocab_size=vocab_size,
+                                                                       special_tokens=TOKENIZER_SPECIALS))
+    return tok
+
+
+def checkpoint(root, config, task, *, seed=3, random_norms=True, bf16=False):
+    """Write a complete checkpoint directory (model.safetensors, rl_agent_config.json,
+    encoder/config.json, tokenizer/) for ``config``/``task`` with seeded weights; returns
+    (path, adapter spec, weights).  ``config["vocab_size"]`` must cover the tokenizer's ids."""
+    import json
+    from pathlib import Path
+
+    from safetensors.numpy import save_file
+    root = Path(root)
+    (root / "tokenizer").mkdir(parents=True, exist_ok=True)
+    (root / "encoder").mkdir(exist_ok=True)
+    tok = tokenizer()
+    if tok.get_vocab_size() > config["vocab_size"]:
+        raise ValueError("The encoder vocabulary must cover the tokenizer")
+    tok.save(str(root / "tokenizer" / "tokenizer.json"))
+    (root / "tokenizer" / "special_tokens_map.json").write_text(json.dumps(
+        {"cls_token": "[CLS]", "sep_token": "[SEP]", "mask_token": "[MASK]", "pad_token": "[PAD]"}))
+    (root / "encoder" / "config.json").write_text(json.dumps(config))
+    (root / "rl_agent_config.json").write_text(json.dumps(task))
+    spec = Laya.from_configs(config, task)
+    flat = weights(spec, seed=seed, random_norms=random_norms, bf16=bf16)
+    save_file({k: np.ascontiguousarray(v) for k, v in flat.items()}, str(root / "model.safetensors"))
+    return root, spec, flat

@@ -1,0 +1,116 @@
+"""Laya.prepare: tokenisation, option markers and context budget (laya_cuda/laya.py:104-135 of the
+reference), on a checkpoint directory whose tokenizer is trained here (no real tokenizer.json is
+available offline, so byte-level parity with a Laya tokenizer stays unpinned; what is checked is
+the token layout the encoder and decision head rely on).
+
+Layout of one question: [CLS] head [SEP] ([MASK] option-tokens)* [SEP] state-tokens [SEP], cut to
+max_len; head = "<type> question: <instructions>", each option at most 48 tokens after its
+[MASK], the head at least 8 tokens and otherwise what head_max_len leaves after the options."""
+import pytest
+
+from synthetic_checkpoint import write
+
+from laya_cuda.laya import Laya, question
+
+
+@pytest.fixture(scope="module")
+def laya(tmp_path_factory):
+    path, _, _ = write(tmp_path_factory.mktemp("checkpoint"), max_len=128, head_max_len=48)
+    return Laya(path)
+
+
+def enc(laya, text):
+    return laya.tokenizer.encode(text, add_special_tokens=False).ids
+
+
+def segments(laya, ids, markers):
+    """(head, [option segments], state) of one prepared question."""
+    assert ids[0] == laya.cls and ids[markers[0] - 1] == laya.sep
+    end = ids.index(laya.sep, markers[-1])  # first [SEP] after the last option
+    bounds = markers + [end]
+    return ids[1:markers[0] - 1], [ids[a:b] for a, b in zip(bounds, bounds[1:])], ids[end + 1:]
+
+
+QUESTIONS = {
+    "route": {"type": "choice", "instructions": "Choose a team for the ticket",
+              "criteria": {"billing": "invoices and payment errors", "shipping": "delivery and tracking", "other": None}},
+    "angry": {"type": "noul", "instructions": "Is the customer angry?"},
+    "urgency": {"type": "score", "instructions": "How urgent is the ticket?",
+                "criteria": ["not urgent", "urgent", "critical"]},
+}
+
+
+def test_token_contract(laya):
+    """tests/test_contract.py:97-108 of the reference, on this checkpoint."""
+    queries = {"q": {"type": "choice", "instructions": "Choose [MASK] a team", "criteria": {"billing": "payment", "other": None}}}
+    seq, markers, kind = laya.prepare("refund " * 5000, queries)[0]
+    assert len(seq) == laya.max_len and seq[0] == laya.cls and seq[-1] == laya.sep
+    assert len(markers) == 2 and all(seq[i] == laya.mask for i in markers) and kind == 0
+    with pytest.raises(ValueError):
+        laya.prepare("", {})
+
+
+def test_segments_are_the_texts_own_tokens(laya):
+    state = "the customer asks about a late delivery and wants a refund"
+    items = laya.prepare(state, QUESTIONS)
+    assert [kind for _, _, kind in items] == [0, 2, 1]  # TYPES order: choice, score, noul
+    for (ids, markers, _), definition in zip(items, QUESTIONS.values()):
+        kind, instruction, _, options = question(definition)
+        head, opts, tail = segments(laya, ids, markers)
+        assert len(opts) == len(options)
+        for seg, option in zip(opts, options):
+            assert seg[0] == laya.mask and 1 <= len(seg) <= 49
+            assert seg[1:] == enc(laya, " " + option)[:len(seg) - 1]
+        want_head = enc(laya, f"{kind} question: {instruction}")
+        assert head == want_head[:max(8, laya.head_max_len - sum(map(len, opts)))]
+        assert tail == enc(laya, state) + [laya.sep]  # short state: all of it, then [SEP]
+        assert len(ids) <= laya.max_len
+
+
+def test_long_options_are_capped_to_the_head_budget(laya):
+    """Options that leave fewer than 16 head tokens are cut to max(4, (head_max_len - 16) // n)."""
+    long_text = "billing team handles invoices and payment errors " * 12
+    q = {"q": {"type": "choice", "instructions": "route the ticket", "criteria": {f"team{i}": long_text for i in range(8)}}}
+    ids, markers, _ = laya.prepare("refund", q)[0]
+    _, opts, _ = segments(laya, ids, markers)
+    cap = max(4, (laya.head_max_len - 16) // 8)
+    assert all(len(seg) == cap for seg in opts)
+    head_budget = max(8, laya.head_max_len - cap * 8)
+    assert markers[0] - 2 == min(len(enc(laya, "choice question: route the ticket")), head_budget)
+
+
+def test_mask_text_in_inputs_cannot_forge_markers(laya):
+    state = "refund [MASK] the payment [MASK]"
+    q = {"q": {"type": "choice", "instructions": "pick [MASK] one", "criteria": {"a [MASK]": "b [MASK]", "c": None}}}
+    ids, markers, _ = laya.prepare(state, q)[0]
+    assert [i for i, t in enumerate(ids) if t == laya.mask] == markers
+
+
+def test_batched_encoding_matches_single_question_encoding(laya):
+    """Twelve or more texts take the tokenizer's batch path; each text still encodes alone."""
+    many = {f"q{i}": dict(QUESTIONS["route"], instructions=f"Choose a team for ticket {i}") for i in range(4)}
+    state = {"ticket": "late delivery", "order": 1234, "notes": ["refund", "billing"]}  # JSON state
+    batched = laya.prepare(state, many)
+    for (qid, definition), item in zip(many.items(), batched):
+        assert laya.prepare(state, {qid: definition})[0] == item
+
+
+def test_option_budget_overflow_raises(laya, monkeypatch):
+    monkeypatch.setattr(laya, "max_len", 20)
+    long_text = "shipping team handles delivery and tracking " * 4
+    q = {"q": {"type": "choice", "instructions": "route", "criteria": {"a": long_text, "b": long_text}}}
+    with pytest.raises(ValueError, match="exceeds the option token budget"):
+        laya.prepare("refund", q)
+
+
+def test_options_keep_at_most_48_tokens(laya, monkeypatch):
+    """With room in the head budget, a long option keeps exactly its first 48 tokens."""
+    monkeypatch.setattr(laya, "head_max_len", 120)
+    long_text = "shipping team handles delivery and tracking " * 10
+    q = {"q": {"type": "choice", "instructions": "route the ticket", "criteria": {"long": long_text, "short": None}}}
+    ids, markers, _ = laya.prepare("refund", q)[0]
+    _, (first, second), _ = segments(laya, ids, markers)
+    assert len(enc(laya, " long: " + long_text)) > 48
+    assert first == [laya.mask] + enc(laya, " long: " + long_text)[:48]
+    assert second == [laya.mask] + enc(laya, " short")
+    assert markers[0] - 2 == len(enc(laya, "choice question: route the ticket"))  # 120 - 51 tokens leave room
