@@ -26,16 +26,23 @@ namespace {
 constexpr int KB = 64;  // keys per block
 
 // One 64-key block of the single-pass softmax for this lane's query q.  s holds the raw QK^T
-// scores of keys kb + 32kt + 8(r/4) + 4g + r%4 (the S^T accumulator layout); the running max
+// scores of keys kb + 32kt + 8(r/4) + 4g + r%4 (the S^T accumulator layout); the reference max
 // `mrow` is kept in the scaled log2 domain (x * log2(e) / 8), so each probability costs one FMA
 // and one exp2.  Keys outside this lane's visible range [qlo, qhi) are masked: the sequence's end,
 // and on local layers the keys farther than the window from the query (kernels.cu:106-107).  Only
 // blocks flagged `edge` by the caller can hold such keys.  The mask is a select per score, not a
-// branch.  A block whose keys are all masked for this query leaves its state untouched.  On return
-// s holds the block's unnormalised probabilities, lsum and o are rescaled.
+// branch.
+//
+// The reference max only moves when a block's max exceeds it by more than 8 (so probabilities
+// stay <= 2^8: exact enough as 16-bit MFMA operands, summed in fp32), and the O/lsum rescale runs
+// only when some lane of the wave moved it: after the first blocks most blocks skip it.  The
+// normaliser uses the same reference as the numerators, so the result is the softmax either way.
+// A block whose keys are all masked for this query leaves its state untouched.  On return s holds
+// the block's unnormalised probabilities, lsum and o are rescaled.
 __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], float& mrow, float& lsum, int kb,
                                               bool edge, int qlo, int qhi, int g) {
   constexpr float c = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) in the exp2 domain
+  constexpr float kSlack = 8.f;                       // log2 of the largest unnormalised probability
   if (edge) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -52,12 +59,21 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], fl
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx[r & 3] = fmaxf(mx[r & 3], s[kt][r]);
   float bmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
-  bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-  const float mnew = fmaxf(mrow, bmax * c);
-  const float base = mnew == -INFINITY ? 0.f : mnew;      // nothing seen yet: probabilities are 0
-  const float alpha = __builtin_amdgcn_exp2f(mrow - base);  // first block: exp2(-inf) = 0
-  mrow = mnew;
-  float part[4] = {0.f, 0.f, 0.f, 0.f};  // four independent sums: a short dependency chain
+  bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64)) * c;
+  const bool grow = bmax > mrow + kSlack;  // false while everything seen so far is masked
+  if (__builtin_amdgcn_ballot_w64(grow)) {
+    // Lanes that keep their reference (including ones that have seen only masked keys) scale by 1;
+    // a lane's first visible block scales its empty state by exp2(-inf) = 0.
+    const float alpha = grow ? __builtin_amdgcn_exp2f(mrow - bmax) : 1.f;
+    mrow = grow ? bmax : mrow;
+    lsum *= alpha;
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+  }
+  const float base = mrow == -INFINITY ? 0.f : mrow;  // nothing seen yet: probabilities are 0
+  float part[4] = {0.f, 0.f, 0.f, 0.f};                // four independent sums: a short dependency chain
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -66,11 +82,7 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], fl
       s[kt][r] = p;
       part[r & 3] += p;
     }
-  lsum = lsum * alpha + ((part[0] + part[1]) + (part[2] + part[3]));
-#pragma unroll
-  for (int d = 0; d < 2; ++d)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
+  lsum += (part[0] + part[1]) + (part[2] + part[3]);
 }
 
 // Workgroup -> (tile, head).  Workgroups are dealt to the 8 XCDs round-robin by linear id; when the
