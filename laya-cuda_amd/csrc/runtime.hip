@@ -13,9 +13,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
-#include <cstdlib>
 #include <list>
-#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -329,135 +327,6 @@ void destroy_slot(Engine& E, Slot* s) {
   delete s;
 }
 
-// GEMM plans for small problems (batch-1 requests, M <= kTuneRows) are measured rather than
-// guessed: at slot creation every valid (tile, split-K) launch shape is timed on the engine's
-// stream with the resident weights and zero-filled scratch operands, and the fastest is kept
-// unless the heuristic plan is within 3% of it (timing noise then does not flip plans).  The
-// choice is cached per process and device, so every engine and slot of a process uses the same
-// plan for the same problem; LAYA_GEMM_TUNE=0 keeps the heuristic plans.  Larger problems keep
-// the heuristic (large tiles first), which the measurements agree with there.
-constexpr int kTuneRows = 2048;
-
-struct TuneScratch {
-  void* a = nullptr;
-  void* out = nullptr;
-  int32_t* positions = nullptr;
-  size_t a_bytes = 0, out_bytes = 0, pos_bytes = 0;
-  hipEvent_t start = nullptr, end = nullptr;
-  ~TuneScratch() {
-    if (a) (void)hipFree(a);
-    if (out) (void)hipFree(out);
-    if (positions) (void)hipFree(positions);
-    if (start) (void)hipEventDestroy(start);
-    if (end) (void)hipEventDestroy(end);
-  }
-  void reserve(void** p, size_t* have, size_t need, hipStream_t stream) {
-    if (*have >= need) return;
-    if (*p) LAYA_HIP(hipFree(*p));
-    *p = nullptr;
-    *have = 0;
-    LAYA_HIP(hipMalloc(p, need));
-    LAYA_HIP(hipMemsetAsync(*p, 0, need, stream));  // finite operands; never captured
-    *have = need;
-  }
-};
-
-bool gemm_tuning_enabled() {
-  const char* v = std::getenv("LAYA_GEMM_TUNE");
-  return !(v && std::strcmp(v, "0") == 0);
-}
-
-std::mutex g_plan_mutex;
-std::map<std::vector<int>, std::pair<int, int>> g_plans;  // (device, M, N, K, epi, dtype, rope) -> (tile, splits)
-
-void plan_gemm(Engine& E, TuneScratch& sc, int M, int N, int K, Epi epi, const void* w, bool rope, int* tile,
-               int* splits) {
-  gemm_plan(M, N, K, epi, E.cus, tile, splits, rope);
-  if (M > kTuneRows || M <= 0 || !gemm_tuning_enabled()) return;
-  const std::vector<int> key{E.device, M, N, K, static_cast<int>(epi), static_cast<int>(E.mfma()), rope ? 1 : 0};
-  {
-    std::lock_guard<std::mutex> lock(g_plan_mutex);
-    auto it = g_plans.find(key);
-    if (it != g_plans.end()) {
-      *tile = it->second.first;
-      *splits = it->second.second;
-      return;
-    }
-  }
-  constexpr int kMaxSplits = 8;
-  const size_t out_elems = epi == Epi::F32 ? static_cast<size_t>(kMaxSplits) * M * N : static_cast<size_t>(M) * N;
-  sc.reserve(&sc.a, &sc.a_bytes, static_cast<size_t>(M) * K * 2, E.stream);
-  sc.reserve(&sc.out, &sc.out_bytes, out_elems * 4, E.stream);
-  sc.reserve(reinterpret_cast<void**>(&sc.positions), &sc.pos_bytes, static_cast<size_t>(M) * 4, E.stream);
-  if (!sc.start) {
-    LAYA_HIP(hipEventCreate(&sc.start));
-    LAYA_HIP(hipEventCreate(&sc.end));
-  }
-  GemmArgs g{};
-  g.a = sc.a;
-  g.b = w;
-  g.M = M;
-  g.N = N;
-  g.K = K;
-  g.lda = K;
-  g.ldb = K;
-  g.ldo = epi == Epi::GEGLU ? N / 2 : N;
-  g.split_stride = static_cast<long long>(M) * N;
-  if (epi == Epi::QKV) {  // q, k and vt side by side in the output scratch
-    const size_t third = static_cast<size_t>(M) * (N / 3) * 2;
-    g.q = sc.out;
-    g.k = static_cast<char*>(sc.out) + third;
-    g.vt = static_cast<char*>(sc.out) + 2 * third;
-    g.width = N / 3;
-    if (rope) {
-      const size_t table = static_cast<size_t>(E.rope_rows) * 32;
-      g.rope_cos = E.rope;
-      g.rope_sin = E.rope + table;
-      g.positions = sc.positions;
-    }
-  } else {
-    g.out = sc.out;
-  }
-  const DType t = E.mfma();
-  auto time_plan = [&](int id, int sp) -> float {
-    g.splits = sp;
-    if (launch_gemm(g, epi, t, id, E.stream) != hipSuccess) {
-      (void)hipGetLastError();
-      return -1.f;
-    }
-    LAYA_HIP(hipEventRecord(sc.start, E.stream));
-    for (int r = 0; r < 3; ++r) LAYA_HIP(launch_gemm(g, epi, t, id, E.stream));
-    LAYA_HIP(hipEventRecord(sc.end, E.stream));
-    LAYA_HIP(hipEventSynchronize(sc.end));
-    float ms = 0.f;
-    LAYA_HIP(hipEventElapsedTime(&ms, sc.start, sc.end));
-    return ms;
-  };
-  const float heuristic = time_plan(*tile, *splits);
-  int best_tile = *tile, best_splits = *splits;
-  float best = heuristic;
-  const int nk = K / 64;
-  for (int id = 0; id < gemm_tile_count(); ++id)
-    for (int sp = 1; sp <= (epi == Epi::F32 ? kMaxSplits : 1); sp *= 2) {
-      if (sp > 1 && nk / sp < 2) continue;
-      if (id == *tile && sp == *splits) continue;
-      const float ms = time_plan(id, sp);
-      if (ms >= 0.f && (best < 0.f || ms < best)) {
-        best = ms;
-        best_tile = id;
-        best_splits = sp;
-      }
-    }
-  if (heuristic >= 0.f && best >= 0.97f * heuristic) {
-    best_tile = *tile;
-    best_splits = *splits;
-  }
-  *tile = best_tile;
-  *splits = best_splits;
-  std::lock_guard<std::mutex> lock(g_plan_mutex);
-  g_plans.emplace(key, std::make_pair(best_tile, best_splits));
-}
-
 Slot* create_slot(Engine& E, int m, int b, int k) {
   const LayaConfig& c = E.cfg;
   Slot* s = new Slot();
@@ -468,29 +337,24 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
   const int d = c.width, f = c.intermediate;
   try {
     const int R = s->L.R;
-    {
-      TuneScratch sc;
-      const Layer& l0 = E.layers[0];
-      plan_gemm(E, sc, m, 3 * d, d, Epi::QKV, l0.wqkv, E.modern, &s->tile[0], &s->splits[0]);
-      plan_gemm(E, sc, m, d, d, Epi::F32, l0.wo, false, &s->tile[1], &s->splits[1]);
-      if (E.modern) {
-        plan_gemm(E, sc, m, 2 * f, d, Epi::GEGLU, l0.wi, false, &s->tile[2], &s->splits[2]);
-      } else {
-        plan_gemm(E, sc, m, f, d, Epi::GELU, l0.wi, false, &s->tile[2], &s->splits[2]);
-      }
-      plan_gemm(E, sc, m, d, f, Epi::F32, l0.wo2, false, &s->tile[3], &s->splits[3]);
-      s->splits[0] = s->splits[2] = 1;
-      if (E.modern) {  // head transformer layers: all rows, then the readout rows of the last one
-        const HeadLayer& h0 = E.head_layers[0];
-        plan_gemm(E, sc, m, 3 * d, d, Epi::QKV, h0.in_w, false, &s->htile[0], &s->hsplits[0]);
-        plan_gemm(E, sc, m, d, d, Epi::F32, h0.out_w, false, &s->htile[1], &s->hsplits[1]);
-        plan_gemm(E, sc, m, 4 * d, d, Epi::RELU, h0.l1_w, false, &s->htile[2], &s->hsplits[2]);
-        plan_gemm(E, sc, m, d, 4 * d, Epi::F32, h0.l2_w, false, &s->htile[3], &s->hsplits[3]);
-        plan_gemm(E, sc, R, d, d, Epi::F32, h0.out_w, false, &s->htile[4], &s->hsplits[4]);
-        plan_gemm(E, sc, R, 4 * d, d, Epi::RELU, h0.l1_w, false, &s->htile[5], &s->hsplits[5]);
-        plan_gemm(E, sc, R, d, 4 * d, Epi::F32, h0.l2_w, false, &s->htile[6], &s->hsplits[6]);
-        s->hsplits[0] = s->hsplits[2] = s->hsplits[5] = 1;
-      }
+    gemm_plan(m, 3 * d, d, Epi::QKV, E.cus, &s->tile[0], &s->splits[0], E.modern);
+    gemm_plan(m, d, d, Epi::F32, E.cus, &s->tile[1], &s->splits[1]);
+    if (E.modern) {
+      gemm_plan(m, 2 * f, d, Epi::GEGLU, E.cus, &s->tile[2], &s->splits[2]);
+    } else {
+      gemm_plan(m, f, d, Epi::GELU, E.cus, &s->tile[2], &s->splits[2]);
+    }
+    gemm_plan(m, d, f, Epi::F32, E.cus, &s->tile[3], &s->splits[3]);
+    s->splits[0] = s->splits[2] = 1;
+    if (E.modern) {  // head transformer layers: all rows, then the readout rows of the last one
+      gemm_plan(m, 3 * d, d, Epi::QKV, E.cus, &s->htile[0], &s->hsplits[0]);
+      gemm_plan(m, d, d, Epi::F32, E.cus, &s->htile[1], &s->hsplits[1]);
+      gemm_plan(m, 4 * d, d, Epi::RELU, E.cus, &s->htile[2], &s->hsplits[2]);
+      gemm_plan(m, d, 4 * d, Epi::F32, E.cus, &s->htile[3], &s->hsplits[3]);
+      gemm_plan(R, d, d, Epi::F32, E.cus, &s->htile[4], &s->hsplits[4]);
+      gemm_plan(R, 4 * d, d, Epi::RELU, E.cus, &s->htile[5], &s->hsplits[5]);
+      gemm_plan(R, d, 4 * d, Epi::F32, E.cus, &s->htile[6], &s->hsplits[6]);
+      s->hsplits[0] = s->hsplits[2] = s->hsplits[5] = 1;
     }
     // Few 128-query tiles (batch-1 requests): split each tile's keys across waves instead of
     // sharing LDS-staged keys between query tiles, so the serial key loop is short.
