@@ -520,7 +520,26 @@ hipError_t gemm_prepare() {
   return e;
 }
 
-void gemm_plan(int M, int N, int K, Epi epi, int cus, int* tile, int* splits, bool rope) {
+// Measured plans: for the batch-1 GEMM problems of the encoder shapes in gemm_plans.inc (written by
+// tune_gemm_plans.py on an MI355X), the (tile, split-K) launch that timed fastest where it beat the
+// heuristic below by more than 3%.  Keyed by CU count, so another part keeps the heuristic.
+struct PlanEntry {
+  int cus, M, N, K, epi, dtype, rope, tile, splits;
+};
+constexpr PlanEntry kPlans[] = {
+#include "gemm_plans.inc"
+    {0, 0, 0, 0, 0, 0, 0, 0, 0},  // end marker
+};
+
+void gemm_plan(int M, int N, int K, Epi epi, DType t, int cus, int* tile, int* splits, bool rope) {
+  for (const PlanEntry& e : kPlans) {
+    if (e.cus == cus && e.M == M && e.N == N && e.K == K && e.epi == static_cast<int>(epi) &&
+        e.dtype == static_cast<int>(t) && e.rope == static_cast<int>(rope) && e.tile < kTileCount) {
+      *tile = e.tile;
+      *splits = e.splits;
+      return;
+    }
+  }
   // Largest tile that still gives every CU a workgroup; small problems fall back to small tiles
   // and, for the fp32 (split-K capable) epilogue, to K splits until the grid covers the chip.
   // Eight-wave tiles first: with two waves per SIMD they sustain the most MFMA throughput when

@@ -76,7 +76,7 @@ int gemm_tile_count();
 GemmTile gemm_tile(int id);
 // Chooses a tile and split count for a problem on `cus` compute units.
 // rope: the QKV epilogue applies RoPE, which needs wave tiles of 64-column multiples.
-void gemm_plan(int M, int N, int K, Epi epi, int cus, int* tile, int* splits, bool rope = false);
+void gemm_plan(int M, int N, int K, Epi epi, DType t, int cus, int* tile, int* splits, bool rope = false);
 hipError_t gemm_prepare();  // sets LDS attributes of the large-tile kernels (call once per device)
 hipError_t launch_gemm(const GemmArgs& a, Epi epi, DType t, int tile, hipStream_t stream);
 

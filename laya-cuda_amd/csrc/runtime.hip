@@ -337,23 +337,23 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
   const int d = c.width, f = c.intermediate;
   try {
     const int R = s->L.R;
-    gemm_plan(m, 3 * d, d, Epi::QKV, E.cus, &s->tile[0], &s->splits[0], E.modern);
-    gemm_plan(m, d, d, Epi::F32, E.cus, &s->tile[1], &s->splits[1]);
+    gemm_plan(m, 3 * d, d, Epi::QKV, E.mfma(), E.cus, &s->tile[0], &s->splits[0], E.modern);
+    gemm_plan(m, d, d, Epi::F32, E.mfma(), E.cus, &s->tile[1], &s->splits[1]);
     if (E.modern) {
-      gemm_plan(m, 2 * f, d, Epi::GEGLU, E.cus, &s->tile[2], &s->splits[2]);
+      gemm_plan(m, 2 * f, d, Epi::GEGLU, E.mfma(), E.cus, &s->tile[2], &s->splits[2]);
     } else {
-      gemm_plan(m, f, d, Epi::GELU, E.cus, &s->tile[2], &s->splits[2]);
+      gemm_plan(m, f, d, Epi::GELU, E.mfma(), E.cus, &s->tile[2], &s->splits[2]);
     }
-    gemm_plan(m, d, f, Epi::F32, E.cus, &s->tile[3], &s->splits[3]);
+    gemm_plan(m, d, f, Epi::F32, E.mfma(), E.cus, &s->tile[3], &s->splits[3]);
     s->splits[0] = s->splits[2] = 1;
     if (E.modern) {  // head transformer layers: all rows, then the readout rows of the last one
-      gemm_plan(m, 3 * d, d, Epi::QKV, E.cus, &s->htile[0], &s->hsplits[0]);
-      gemm_plan(m, d, d, Epi::F32, E.cus, &s->htile[1], &s->hsplits[1]);
-      gemm_plan(m, 4 * d, d, Epi::RELU, E.cus, &s->htile[2], &s->hsplits[2]);
-      gemm_plan(m, d, 4 * d, Epi::F32, E.cus, &s->htile[3], &s->hsplits[3]);
-      gemm_plan(R, d, d, Epi::F32, E.cus, &s->htile[4], &s->hsplits[4]);
-      gemm_plan(R, 4 * d, d, Epi::RELU, E.cus, &s->htile[5], &s->hsplits[5]);
-      gemm_plan(R, d, 4 * d, Epi::F32, E.cus, &s->htile[6], &s->hsplits[6]);
+      gemm_plan(m, 3 * d, d, Epi::QKV, E.mfma(), E.cus, &s->htile[0], &s->hsplits[0]);
+      gemm_plan(m, d, d, Epi::F32, E.mfma(), E.cus, &s->htile[1], &s->hsplits[1]);
+      gemm_plan(m, 4 * d, d, Epi::RELU, E.mfma(), E.cus, &s->htile[2], &s->hsplits[2]);
+      gemm_plan(m, d, 4 * d, Epi::F32, E.mfma(), E.cus, &s->htile[3], &s->hsplits[3]);
+      gemm_plan(R, d, d, Epi::F32, E.mfma(), E.cus, &s->htile[4], &s->hsplits[4]);
+      gemm_plan(R, 4 * d, d, Epi::RELU, E.mfma(), E.cus, &s->htile[5], &s->hsplits[5]);
+      gemm_plan(R, d, 4 * d, Epi::F32, E.mfma(), E.cus, &s->htile[6], &s->hsplits[6]);
       s->hsplits[0] = s->hsplits[2] = s->hsplits[5] = 1;
     }
     // Few 128-query tiles (batch-1 requests): split each tile's keys across waves instead of
@@ -1214,7 +1214,7 @@ int laya_op_linear(const void* x, const void* w, const float* bias, void* out, i
                                                                                                     : Epi::GEGLU;
     int cus = 256;
     if (tile < 0) {
-      gemm_plan(M, N, K, epi, cus, &tile, &splits);
+      gemm_plan(M, N, K, epi, half_type(dtype16), cus, &tile, &splits);
       if (bias) splits = 1;
     }
     LAYA_REQUIRE(tile < gemm_tile_count(), "bad tile id");
@@ -1235,7 +1235,7 @@ int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* 
     int splits = 1;
     const bool rope = rope_cos != nullptr;
     LAYA_REQUIRE(!rope || (rope_sin && positions), "RoPE needs cos, sin and positions");
-    if (tile < 0) gemm_plan(M, 3 * width, width, Epi::QKV, 256, &tile, &splits, rope);
+    if (tile < 0) gemm_plan(M, 3 * width, width, Epi::QKV, half_type(dtype16), 256, &tile, &splits, rope);
     LAYA_REQUIRE(tile < gemm_tile_count(), "bad tile id");
     LAYA_REQUIRE(width % 64 == 0 && (3 * width) % gemm_tile(tile).bn == 0, "width does not fit the tile");
     LAYA_REQUIRE(M % 8 == 0, "rows must be a multiple of 8 (V^T is stored in runs of 8 tokens)");
