@@ -4,13 +4,16 @@
 // cublasGemmEx orientation at laya_cuda/ops.py:63-64), which is exactly what the gfx950
 // v_mfma_f32_32x32x16_{bf16,f16} operands want: each lane feeds 8 consecutive k of one row.
 //
-// Workgroup: 4 or 8 waves on a WM x WN grid; each wave owns (BM/WM) x (BN/WN) made of
-// 32x32 MFMA tiles (8 waves put two waves on each SIMD of the CU, so one issues MFMAs while the
-// other waits on LDS or a barrier).  K advances in 64-wide slabs staged through LDS, double-buffered; the global
-// loads of the next PF slabs are in flight in registers while the current slab feeds the MFMAs,
-// and each lands in the other LDS buffer one slab before its use; one barrier per slab.  LDS rows are 128 B (64 x 16-bit) with the
-// 16-byte chunk index XOR-swizzled by (row & 7), so the 32 lanes reading one k-chunk of 32
-// consecutive rows hit distinct banks.
+// Workgroup: 4 or 8 waves on a WM x WN grid; each wave owns (BM/WM) x (BN/WN) made of 32x32 MFMA
+// tiles (8 waves put two waves on each SIMD of the CU, so one issues MFMAs while the other waits on
+// LDS or a barrier).  Two main loops share one epilogue:
+//   gemm_kernel       small tiles (batch-1 problems): 64-deep K slabs staged through registers into
+//                     two LDS buffers, PF slabs of global loads in flight;
+//   gemm_pipe_kernel  large tiles (batched problems): an S-stage pipeline of K slabs loaded straight
+//                     from global memory into LDS, LDS fragment reads of the next k-step overlapped
+//                     with the MFMAs of the current one.
+// LDS rows hold one slab row with the 16-byte chunk index XOR-swizzled (swz, swz_k below), so the
+// lanes reading one k-chunk of consecutive rows hit distinct banks.
 //
 // Epilogues (all fp32 until the single final rounding, bias added before it as in
 // laya_cuda/kernels.cu:50-55):
@@ -29,6 +32,14 @@ namespace laya {
 namespace {
 
 constexpr int BK = 64;
+
+// LDS tiles: rows of BK 16-bit elements (128 B) as eight 16-byte chunks, the chunk index
+// XOR-swizzled by (row / 2) % 8.  A 16-byte LDS read is served 16 lanes per pass from 64 banks
+// (256 B); the 16 lanes of a pass fetch the same k-chunk of 16 consecutive rows, i.e. eight
+// 256-byte row pairs, and (row / 2) % 8 puts those eight pairs on eight different chunk
+// positions (measured on gfx950: swizzling by row % 8 instead leaves the two rows 8 apart on the
+// same banks, and rocprof's SQ_LDS_BANK_CONFLICT counts stalls for half of all LDS cycles).
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 
 // Workgroup tile coordinates.  Workgroups are dealt to the 8 XCDs round-robin by linear dispatch
 // id, so consecutive ids run on different L2s.  When the workgroup count allows, the logical index
@@ -60,196 +71,20 @@ __device__ __forceinline__ void tile_coords(int nx, int ny, int nz, bool rows_ma
   }
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int PF, Epi E>
-__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
-  constexpr int NT = 64 * WM * WN;
-  static_assert(WM * WN == 4 || WM * WN == 8, "four or eight waves per workgroup");
-  static_assert(PF >= 1, "at least one slab in flight");
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int TM = WTM / 32, TN = WTN / 32;
-  static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "32x32 MFMA tiles");
-  constexpr int ACH = BM * 8 / NT;  // 16-byte chunks per thread per slab
-  constexpr int BCH = BN * 8 / NT;
-  static_assert(ACH >= 1 && BCH >= 1 && ACH * NT == BM * 8 && BCH * NT == BN * 8, "whole chunks per thread");
-  typedef typename Vec8<T>::type T8;
+// Bytes of LDS the epilogue stages through: one 32 x 36 fp32 (or 32 x 40 16-bit) region per wave.
+constexpr int kEpilogueStageBytes = 32 * 36 * 4;
 
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* sA = reinterpret_cast<T*>(smem_raw);
-  T* sB = sA + 2 * BM * BK;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// Epilogue shared by both GEMM kernels: acc holds this wave's (BM/WM) x (BN/WN) block of C^T as
+// 32x32 MFMA tiles; smem_raw must have kEpilogueStageBytes per wave free (the caller's main loop is
+// done with LDS: its last barrier has passed).
+template <typename T, int BM, int BN, int WM, int WN, Epi E, bool kEarlyBias>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
+                                              const float4 (&early_bias)[4], int m0, int n0, int z,
+                                              unsigned char* smem_raw, int lane, int wave) {
+  constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
-  int tx, ty, z;
-  tile_coords(gridDim.x, gridDim.y, gridDim.z, a.rows_major, &tx, &ty, &z);
-  const int n0 = tx * BN, m0 = ty * BM;
-
-  const T* A = static_cast<const T*>(a.a);
-  const T* B = static_cast<const T*>(a.b);
-  const int nk = a.K / BK;
-  const int per = (nk + a.splits - 1) / a.splits;
-  const int kb = z * per, ke = min(nk, kb + per);
-
-  auto gload = [&](int kt, i32x4 (&xa)[ACH], i32x4 (&xb)[BCH]) {
-    const int k0 = kt * BK;
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
-      const int g = min(m0 + row, a.M - 1);
-      xa[i] = *reinterpret_cast<const i32x4*>(A + static_cast<size_t>(g) * a.lda + k0 + ch * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
-      xb[i] = *reinterpret_cast<const i32x4*>(B + static_cast<size_t>(n0 + row) * a.ldb + k0 + ch * 8);
-    }
-  };
-  auto lstore = [&](int buf, const i32x4 (&xa)[ACH], const i32x4 (&xb)[BCH]) {
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
-      *reinterpret_cast<i32x4*>(sA + buf * BM * BK + row * BK + ((ch ^ (row & 7)) << 3)) = xa[i];
-    }
-#pragma unroll
-    for (int i = 0; i < BCH; ++i) {
-      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
-      *reinterpret_cast<i32x4*>(sB + buf * BN * BK + row * BK + ((ch ^ (row & 7)) << 3)) = xb[i];
-    }
-  };
-
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
   const int lrow = lane & 31, kg = lane >> 5;
-  // Small wave tiles fetch their bias at kernel start (16 floats per 32 columns per lane), so its
-  // latency hides under the main loop instead of opening the epilogue.
-  constexpr bool kEarlyBias = TN == 1;
   const bool with_bias = (E != Epi::F32 || a.splits == 1) && a.bias;
-  float4 early_bias[4];
-  if constexpr (kEarlyBias) {
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4)
-      early_bias[r4] = with_bias ? *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + 8 * r4 + 4 * kg)
-                                 : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-  // One 64-deep slab from LDS buffer `buf`: four 16-deep MFMA steps.  With at most 8 MFMA tiles per
-  // wave the fragments are double-buffered in registers, so the LDS reads of step kk+1 are in
-  // flight while the MFMAs of step kk run; larger wave tiles have no registers to spare for that.
-  constexpr bool kFrag2 = TM * TN <= 8;
-  auto compute = [&](int buf) {
-    const T* cA = sA + buf * BM * BK;
-    const T* cB = sB + buf * BN * BK;
-    T8 af[kFrag2 ? 2 : 1][TM], bfr[kFrag2 ? 2 : 1][TN];
-    auto fetch = [&](int kk, int s) {
-      const int ch = kk * 2 + kg;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm0 + i * 32 + lrow;
-        af[s][i] = *reinterpret_cast<const T8*>(cA + r * BK + ((ch ^ (r & 7)) << 3));
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int r = wn0 + j * 32 + lrow;
-        bfr[s][j] = *reinterpret_cast<const T8*>(cB + r * BK + ((ch ^ (r & 7)) << 3));
-      }
-    };
-    if constexpr (kFrag2) fetch(0, 0);
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int s = kFrag2 ? (kk & 1) : 0;
-      if constexpr (kFrag2) {
-        if (kk + 1 < BK / 16) fetch(kk + 1, (kk + 1) & 1);
-      } else {
-        fetch(kk, 0);
-      }
-      // Weights as the MFMA A operand: the accumulator holds C^T, so each lane ends with four
-      // consecutive output columns of one row.
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(bfr[s][j], af[s][i], acc[i][j]);
-    }
-  };
-
-  const int n = ke - kb;
-  if constexpr (PF == 1) {
-    // Large tiles: slabs go from global memory straight into LDS (global_load_lds_dwordx4: no
-    // register staging, no LDS store instructions).  Slab it+1 is loaded into the other buffer
-    // while slab it feeds the MFMAs; each wave waits for its own loads, then one barrier makes the
-    // slab visible to all.  A load instruction fills 1 KB of LDS = 8 rows of 128 B, lane l at row
-    // l/8, physical 16-byte chunk l%8, so lane l fetches logical chunk (l%8) ^ (l/8): the same
-    // XOR-swizzled layout as the register path.
-    typedef __attribute__((address_space(3))) void* LdsPtr;
-    typedef __attribute__((address_space(1))) void* GlobalPtr;
-    constexpr int NW = WM * WN;
-    constexpr int AG = BM / 8 / NW, BG = BN / 8 / NW;  // 8-row groups per wave per slab
-    static_assert(AG * 8 * NW == BM && BG * 8 * NW == BN, "whole 8-row groups per wave");
-    const int lr = lane >> 3, lch = (lane & 7) ^ lr;
-    auto dload = [&](int kt, int buf) {
-      const int k0 = kt * BK + lch * 8;
-#pragma unroll
-      for (int i = 0; i < AG; ++i) {
-        const int grp = wave + NW * i;
-        const int g = min(m0 + grp * 8 + lr, a.M - 1);  // rows past M read row M-1, never stored
-        __builtin_amdgcn_global_load_lds((GlobalPtr)(A + static_cast<size_t>(g) * a.lda + k0),
-                                         (LdsPtr)(sA + buf * BM * BK + grp * 8 * BK), 16, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < BG; ++i) {
-        const int grp = wave + NW * i;
-        __builtin_amdgcn_global_load_lds((GlobalPtr)(B + static_cast<size_t>(n0 + grp * 8 + lr) * a.ldb + k0),
-                                         (LdsPtr)(sB + buf * BN * BK + grp * 8 * BK), 16, 0, 0);
-      }
-    };
-    // s_waitcnt immediate for vmcnt(0) with expcnt and lgkmcnt left free (gfx9 field layout).
-    constexpr int kVmcnt0 = 0x0F70;
-    if (n > 0) {
-      dload(kb, 0);
-      __builtin_amdgcn_s_waitcnt(kVmcnt0);
-      __syncthreads();
-      for (int it = 0; it < n; ++it) {
-        if (it + 1 < n) dload(kb + it + 1, (it + 1) & 1);
-        compute(it & 1);
-        __builtin_amdgcn_s_waitcnt(kVmcnt0);
-        __syncthreads();
-      }
-    }
-  } else {
-    // Small tiles (batch-1 problems): slab s >= 1 travels in register set (s-1) % PF, issued PF
-    // slabs ahead of its use, so PF slabs of global loads are in flight while the MFMAs consume the
-    // slab in LDS.  Two LDS buffers; one barrier per slab.  Every step issues its loads
-    // unconditionally (slab indices past the end are clamped to the last slab and never used), so
-    // the number of loads in flight is the same on every path and the compiler's wait counts keep
-    // the PF-1 younger sets in flight.
-    if (n > 0) {
-      i32x4 ra[PF][ACH], rb[PF][BCH];
-      auto step = [&](int it, int u) {
-        compute(it & 1);
-        lstore((it + 1) & 1, ra[u], rb[u]);  // at it = n-1 this fills the idle buffer; never read
-        gload(kb + min(it + 1 + PF, n - 1), ra[u], rb[u]);
-        __syncthreads();
-      };
-      gload(kb, ra[0], rb[0]);
-      lstore(0, ra[0], rb[0]);
-#pragma unroll
-      for (int p = 0; p < PF; ++p) gload(kb + min(1 + p, n - 1), ra[p], rb[p]);
-      __syncthreads();
-      int it = 0;
-      for (; it + PF <= n; it += PF) {
-#pragma unroll
-        for (int u = 0; u < PF; ++u) step(it + u, u);
-      }
-#pragma unroll
-      for (int u = 0; u < PF; ++u)
-        if (it + u < n) step(it + u, u);
-    }
-    __syncthreads();  // the epilogue reuses LDS
-  }
-
   // Epilogue.  Element r of lane l in a 32x32 tile of C^T is output column 8*(r/4) + 4*(l/32) +
   // r%4 of output row l%32: a lane holds columns c..c+3 of one row for each r/4.  The bias joins in
   // fp32 before the single rounding.
@@ -299,8 +134,6 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
   // execute in issue order, so the region needs no barrier between writes and reads.
   constexpr int SP = E == Epi::F32 ? 36 : 40;  // stage pitch in elements: 144 B / 80 B, 16-byte aligned
   typedef typename std::conditional<E == Epi::F32, float, T>::type S;
-  static_assert(static_cast<size_t>(WM * WN) * 32 * SP * sizeof(S) <= static_cast<size_t>(2) * (BM + BN) * BK * 2,
-                "the staging regions fit in the main loop's LDS");
   S* stg = reinterpret_cast<S*>(smem_raw) + wave * 32 * SP;
   const int rbase = m0 + wm0;  // first output row of this wave
   // Row-major 32x32 tile: lane values h[r4] = columns 8 r4 + 4 kg .. +3 of tile row lrow; chunk
@@ -431,50 +264,418 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
   }
 }
 
+template <typename T, int BM, int BN, int WM, int WN, int PF, Epi E>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
+  constexpr int NT = 64 * WM * WN;
+  static_assert(WM * WN == 4 || WM * WN == 8, "four or eight waves per workgroup");
+  static_assert(PF >= 2, "register-staged slabs in flight (large tiles use gemm_pipe_kernel)");
+  static_assert(WM * WN * kEpilogueStageBytes <= 2 * (BM + BN) * BK * 2, "the epilogue's staging fits the LDS");
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "32x32 MFMA tiles");
+  constexpr int ACH = BM * 8 / NT;  // 16-byte chunks per thread per slab
+  constexpr int BCH = BN * 8 / NT;
+  static_assert(ACH >= 1 && BCH >= 1 && ACH * NT == BM * 8 && BCH * NT == BN * 8, "whole chunks per thread");
+  typedef typename Vec8<T>::type T8;
+
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* sA = reinterpret_cast<T*>(smem_raw);
+  T* sB = sA + 2 * BM * BK;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+  int tx, ty, z;
+  tile_coords(gridDim.x, gridDim.y, gridDim.z, a.rows_major, &tx, &ty, &z);
+  const int n0 = tx * BN, m0 = ty * BM;
+
+  const T* A = static_cast<const T*>(a.a);
+  const T* B = static_cast<const T*>(a.b);
+  const int nk = a.K / BK;
+  const int per = (nk + a.splits - 1) / a.splits;
+  const int kb = z * per, ke = min(nk, kb + per);
+
+  auto gload = [&](int kt, i32x4 (&xa)[ACH], i32x4 (&xb)[BCH]) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
+      const int g = min(m0 + row, a.M - 1);
+      xa[i] = *reinterpret_cast<const i32x4*>(A + static_cast<size_t>(g) * a.lda + k0 + ch * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
+      xb[i] = *reinterpret_cast<const i32x4*>(B + static_cast<size_t>(n0 + row) * a.ldb + k0 + ch * 8);
+    }
+  };
+  auto lstore = [&](int buf, const i32x4 (&xa)[ACH], const i32x4 (&xb)[BCH]) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
+      *reinterpret_cast<i32x4*>(sA + buf * BM * BK + row * BK + ((ch ^ swz(row)) << 3)) = xa[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BCH; ++i) {
+      const int c = tid + NT * i, row = c >> 3, ch = c & 7;
+      *reinterpret_cast<i32x4*>(sB + buf * BN * BK + row * BK + ((ch ^ swz(row)) << 3)) = xb[i];
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int lrow = lane & 31, kg = lane >> 5;
+  // Small wave tiles fetch their bias at kernel start (16 floats per 32 columns per lane), so its
+  // latency hides under the main loop instead of opening the epilogue.
+  constexpr bool kEarlyBias = TN == 1;
+  const bool with_bias = (E != Epi::F32 || a.splits == 1) && a.bias;
+  float4 early_bias[4];
+  if constexpr (kEarlyBias) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+      early_bias[r4] = with_bias ? *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + 8 * r4 + 4 * kg)
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  // One 64-deep slab from LDS buffer `buf`: four 16-deep MFMA steps.  With at most 8 MFMA tiles per
+  // wave the fragments are double-buffered in registers, so the LDS reads of step kk+1 are in
+  // flight while the MFMAs of step kk run; larger wave tiles have no registers to spare for that.
+  constexpr bool kFrag2 = TM * TN <= 8;
+  auto compute = [&](int buf) {
+    const T* cA = sA + buf * BM * BK;
+    const T* cB = sB + buf * BN * BK;
+    T8 af[kFrag2 ? 2 : 1][TM], bfr[kFrag2 ? 2 : 1][TN];
+    auto fetch = [&](int kk, int s) {
+      const int ch = kk * 2 + kg;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm0 + i * 32 + lrow;
+        af[s][i] = *reinterpret_cast<const T8*>(cA + r * BK + ((ch ^ swz(r)) << 3));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int r = wn0 + j * 32 + lrow;
+        bfr[s][j] = *reinterpret_cast<const T8*>(cB + r * BK + ((ch ^ swz(r)) << 3));
+      }
+    };
+    if constexpr (kFrag2) fetch(0, 0);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int s = kFrag2 ? (kk & 1) : 0;
+      if constexpr (kFrag2) {
+        if (kk + 1 < BK / 16) fetch(kk + 1, (kk + 1) & 1);
+      } else {
+        fetch(kk, 0);
+      }
+      // Weights as the MFMA A operand: the accumulator holds C^T, so each lane ends with four
+      // consecutive output columns of one row.
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(bfr[s][j], af[s][i], acc[i][j]);
+    }
+  };
+
+  const int n = ke - kb;
+  {
+    // Small tiles (batch-1 problems): slab s >= 1 travels in register set (s-1) % PF, issued PF
+    // slabs ahead of its use, so PF slabs of global loads are in flight while the MFMAs consume the
+    // slab in LDS.  Two LDS buffers; one barrier per slab.  Every step issues its loads
+    // unconditionally (slab indices past the end are clamped to the last slab and never used), so
+    // the number of loads in flight is the same on every path and the compiler's wait counts keep
+    // the PF-1 younger sets in flight.
+    if (n > 0) {
+      i32x4 ra[PF][ACH], rb[PF][BCH];
+      auto step = [&](int it, int u) {
+        compute(it & 1);
+        lstore((it + 1) & 1, ra[u], rb[u]);  // at it = n-1 this fills the idle buffer; never read
+        gload(kb + min(it + 1 + PF, n - 1), ra[u], rb[u]);
+        __syncthreads();
+      };
+      gload(kb, ra[0], rb[0]);
+      lstore(0, ra[0], rb[0]);
+#pragma unroll
+      for (int p = 0; p < PF; ++p) gload(kb + min(1 + p, n - 1), ra[p], rb[p]);
+      __syncthreads();
+      int it = 0;
+      for (; it + PF <= n; it += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) step(it + u, u);
+      }
+#pragma unroll
+      for (int u = 0; u < PF; ++u)
+        if (it + u < n) step(it + u, u);
+    }
+    __syncthreads();  // the epilogue reuses LDS
+  }
+
+  gemm_epilogue<T, BM, BN, WM, WN, E, kEarlyBias>(a, acc, early_bias, m0, n0, z, smem_raw, lane, wave);
+}
+
+// LDS layout of the pipelined kernel: rows of BKS 16-bit elements, CPR = BKS / 8 chunks of 16 B per
+// row, the chunk index XOR-swizzled by (row / (16 / CPR)) % CPR.  The 16 lanes of one LDS read
+// pass fetch the same k-chunk of 16 consecutive rows; 16 / CPR rows fill one 256-byte line of the
+// 64 banks, and the swizzle gives the rows that share a position in that line distinct chunks, so
+// the pass touches 16 distinct 16-byte bank groups (BKS = 64: the swz above).
+template <int BKS>
+__device__ __forceinline__ int swz_k(int row) {
+  constexpr int CPR = BKS / 8;
+  return (row / (16 / CPR)) % CPR;
+}
+
+// Large tiles (batched problems): a multi-stage pipeline of K slabs moved from global memory
+// straight into LDS (global_load_lds_dwordx4: no register staging, no LDS store instructions).
+// A load instruction fills 1 KB of LDS = 64 / CPR rows, lane l at row l / CPR of its group and
+// physical chunk l % CPR, fetching the logical chunk (l % CPR) ^ swz_k(row).
+//
+// S LDS stages hold slabs it .. it+S-2 while slab it is consumed; per slab (KS = BKS / 16 k-steps):
+//   k-steps 0..KS-2: LDS fragments of step kk+1 are read while the MFMAs of step kk run (two
+//                    register sets); the direct loads of slab it+S-1 (into the stage slab it-1
+//                    used) are spread over these steps;
+//   then each wave waits until its own loads of slab it+1 have landed (those of the S-2 younger
+//   slabs stay in flight) and its own LDS reads are done, and one barrier makes slab it+1 visible
+//   and frees stage it for the loads issued in the next slab;
+//   k-step KS-1: its fragments are already in registers, so its MFMAs start right after the
+//                barrier while step 0 of slab it+1 is read.
+// Loads are issued unconditionally (slab indices past the end are clamped to the last slab and
+// land in a stage that is never read again), so the loop body is one straight-line block that the
+// scheduling-group hints interleave: one MFMA, then one LDS read or one global load, so neither
+// queue starves the matrix pipe.  Two waves per SIMD (register budget 256), except for 128x128
+// wave tiles whose accumulators alone take 256 registers: 8-wave workgroups own a CU, 4-wave ones
+// with smaller wave tiles share it with a second workgroup (whose main loop then covers this one's
+// epilogue).
+template <typename T, int BM, int BN, int WM, int WN, int BKS, int S, Epi E>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(BM * BN / (WM * WN) >= 128 * 128 ? 1 : 2)))
+void gemm_pipe_kernel(GemmArgs a) {
+  constexpr int NW = WM * WN;
+  static_assert(NW == 4 || NW == 8, "four or eight waves per workgroup");
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1 && WTM % 32 == 0 && WTN % 32 == 0, "32x32 MFMA tiles");
+  constexpr int CPR = BKS / 8, RPI = 64 / CPR, KS = BKS / 16;
+  static_assert(BKS == 32 || BKS == 64, "32- or 64-deep slabs");
+  constexpr int AG = BM / RPI / NW, BG = BN / RPI / NW, NLD = AG + BG;  // load instructions per wave per slab
+  static_assert(AG * RPI * NW == BM && BG * RPI * NW == BN, "whole load groups per wave");
+  static_assert(S >= 2, "at least two stages");
+  constexpr int SLAB = (BM + BN) * BKS;  // 16-bit elements per stage: A rows, then B rows
+  static_assert(NW * kEpilogueStageBytes <= S * SLAB * 2, "the epilogue's staging fits the LDS");
+  constexpr int kKeep = NLD * (S - 2);  // loads of younger slabs that stay in flight at a slab's end
+  static_assert(kKeep < 64, "vmcnt range");
+  // s_waitcnt vmcnt(kKeep) lgkmcnt(0), expcnt left free (gfx9 field layout: vmcnt bits 3:0 and 15:14)
+  constexpr int kWaitSlab = (kKeep & 15) | ((kKeep >> 4) << 14) | (7 << 4);
+  constexpr int kWaitAll = 7 << 4;
+  typedef typename Vec8<T>::type T8;
+  typedef __attribute__((address_space(3))) void* LdsPtr;
+  typedef __attribute__((address_space(1))) void* GlobalPtr;
+
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* const lds = reinterpret_cast<T*>(smem_raw);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+  int tx, ty, z;
+  tile_coords(gridDim.x, gridDim.y, gridDim.z, a.rows_major, &tx, &ty, &z);
+  const int n0 = tx * BN, m0 = ty * BM;
+
+  const int nk = a.K / BKS;
+  const int per = (nk + a.splits - 1) / a.splits;
+  const int kb = z * per, ke = min(nk, kb + per);
+  const int n = ke - kb;
+
+  // Per-lane source of each of this wave's load instructions (slab 0) and its LDS offset.
+  const T* src[NLD];
+  int dst[NLD];
+  {
+    const int lr = lane / CPR, pch = lane % CPR;
+    const T* A = static_cast<const T*>(a.a);
+    const T* B = static_cast<const T*>(a.b);
+#pragma unroll
+    for (int q = 0; q < NLD; ++q) {
+      const bool isA = q < AG;
+      const int grp = wave + NW * (isA ? q : q - AG);
+      const int row = grp * RPI + lr;
+      const int ch = pch ^ swz_k<BKS>(row);
+      if (isA) {
+        const int g = min(m0 + row, a.M - 1);  // rows past M read row M-1, never stored
+        src[q] = A + static_cast<size_t>(g) * a.lda + ch * 8;
+        dst[q] = grp * RPI * BKS;
+      } else {
+        src[q] = B + static_cast<size_t>(n0 + row) * a.ldb + ch * 8;
+        dst[q] = BM * BKS + grp * RPI * BKS;
+      }
+    }
+  }
+  // The loads are issued from inline assembly: the compiler's own global_load_lds makes its wait
+  // counter model assume each one may overwrite any LDS a pending read targets, so it drains all LDS
+  // reads before every load and serialises the fragment reads of the next k-step with the MFMAs.
+  // Here the stage a load writes is never read until after a barrier that follows an explicit
+  // s_waitcnt on those loads, so no such wait is needed.  M0 holds the LDS destination of the
+  // instruction (one s_nop after writing it before the LDS DMA reads it).
+  const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>((LdsPtr)smem_raw));
+  auto issue = [&](int q, int kt, int st) {
+    const T* g = src[q] + static_cast<size_t>(kt) * BKS;
+    const unsigned m0 = lds_base + static_cast<unsigned>(st * SLAB + dst[q]) * 2;
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "m0");
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int lrow = lane & 31, kg = lane >> 5;
+  T8 af[2][TM], bfr[2][TN];
+  auto fetch = [&](int st, int kk, int s) {
+    const T* cA = lds + st * SLAB;
+    const T* cB = cA + BM * BKS;
+    const int ch = kk * 2 + kg;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm0 + i * 32 + lrow;
+      af[s][i] = *reinterpret_cast<const T8*>(cA + r * BKS + ((ch ^ swz_k<BKS>(r)) << 3));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int r = wn0 + j * 32 + lrow;
+      bfr[s][j] = *reinterpret_cast<const T8*>(cB + r * BKS + ((ch ^ swz_k<BKS>(r)) << 3));
+    }
+  };
+  // Weights as the MFMA A operand: the accumulator holds C^T, so each lane ends with four
+  // consecutive output columns of one row.
+  auto mma = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(bfr[s][j], af[s][i], acc[i][j]);
+  };
+  constexpr int NMF = TM * TN, NDS = TM + TN;
+  // Interleave hint for one k-step: NMF MFMAs, NDS LDS reads and `nvm` global loads.  The LDS reads
+  // go first, two per MFMA, so the fragments of the next step have most of this step's MFMAs to
+  // land; the global loads fill the slots after the later MFMAs.
+  constexpr int DPM = 2;  // LDS reads issued per MFMA slot
+  auto interleave = [&](auto nvm_c) {
+    constexpr int nvm = decltype(nvm_c)::value;
+#pragma unroll
+    for (int t = 0; t < NMF; ++t) {
+#pragma unroll
+      for (int d = 0; d < DPM; ++d)
+        if (t * DPM + d < NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                        // one MFMA
+      const int v = t - (NMF - nvm);
+      if (v >= 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global load
+    }
+  };
+  // The NLD loads of a slab are spread over the KS-1 k-steps before the barrier.
+  constexpr int KPRE = KS - 1;
+  constexpr int LPS = (NLD + KPRE - 1) / KPRE;  // loads per pre-barrier k-step
+  static_assert(LPS <= NMF, "loads fit the MFMA slots");
+
+  if (n > 0) {
+#pragma unroll
+    for (int p = 0; p < S - 1; ++p)
+#pragma unroll
+      for (int q = 0; q < NLD; ++q) issue(q, kb + min(p, n - 1), p);
+    __builtin_amdgcn_s_waitcnt(kWaitSlab);
+    __builtin_amdgcn_s_barrier();
+    fetch(0, 0, 0);
+    int cur = 0, ldst = S - 1;  // stage of slab it, stage receiving slab it+S-1
+    for (int it = 0; it < n; ++it) {
+      const int lslab = kb + min(it + S - 1, n - 1);
+      const int nxt = cur + 1 == S ? 0 : cur + 1;
+#pragma unroll
+      for (int kk = 0; kk < KPRE; ++kk) {
+#pragma unroll
+        for (int q = kk * LPS; q < (kk + 1) * LPS && q < NLD; ++q) issue(q, lslab, ldst);
+        fetch(cur, kk + 1, (kk + 1) & 1);
+        mma(kk & 1);
+        constexpr int nvm_max = LPS;
+        interleave(std::integral_constant<int, nvm_max>());
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitSlab);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      fetch(nxt, 0, 0);
+      mma((KS - 1) & 1);
+      interleave(std::integral_constant<int, 0>());
+      __builtin_amdgcn_sched_barrier(0);
+      cur = nxt;
+      ldst = ldst + 1 == S ? 0 : ldst + 1;
+    }
+  }
+  // The clamped loads of the last slabs may still be landing: drain them before the epilogue
+  // reuses LDS.
+  __builtin_amdgcn_s_waitcnt(kWaitAll);
+  __syncthreads();
+  const float4 no_bias[4] = {};
+  gemm_epilogue<T, BM, BN, WM, WN, E, false>(a, acc, no_bias, m0, n0, z, smem_raw, lane, wave);
+}
+
 struct TileDef {
-  int bm, bn, wm, wn, pf;
+  int bm, bn, wm, wn;
+  int pf;      // >= 2: register-staged kernel with pf slabs in flight; 0: pipelined direct-to-LDS kernel
+  int bk, st;  // pipelined kernel: slab depth and LDS stages
   int threads() const { return 64 * wm * wn; }
 };
 // Tile menu; the planner picks per problem.  Ids are part of the op-level ABI (tests sweep them).
-// pf = K slabs of global loads in flight: deep for the small tiles of batch-1 problems, whose few
-// MFMAs per slab cannot cover HBM latency, shallow for the large tiles of batched problems.
+// Register-staged tiles keep pf K slabs of global loads in flight (deep for the small tiles of
+// batch-1 problems, whose few MFMAs per slab cannot cover HBM latency); pipelined tiles keep st-1.
 constexpr TileDef kTiles[] = {
-    {256, 256, 2, 2, 1},  // 0: wave 128x128, large M (batched)
-    {256, 128, 2, 2, 1},  // 1: wave 128x64
-    {128, 128, 2, 2, 2},  // 2: wave 64x64
-    {128, 64, 2, 2, 3},   // 3: wave 64x32
-    {64, 128, 2, 2, 3},   // 4: wave 32x64
-    {64, 64, 2, 2, 4},    // 5: wave 32x32, small M (batch-1 latency)
-    {32, 128, 1, 4, 4},   // 6: wave 32x32, very small M
-    {256, 256, 2, 4, 1},  // 7: 8 waves of 128x64, large M
-    {256, 128, 4, 2, 1},  // 8: 8 waves of 64x64
-    {128, 256, 2, 4, 1},  // 9: 8 waves of 64x64
-    {128, 64, 4, 1, 3},   // 10: wave 32x64, whole heads per wave for RoPE when N is not a multiple of 128
+    {256, 256, 2, 2, 0, 64, 2},  // 0: 4 waves of 128x128, large M (batched)
+    {256, 128, 2, 2, 0, 64, 2},  // 1: 4 waves of 128x64
+    {128, 128, 2, 2, 2, 64, 0},  // 2: wave 64x64
+    {128, 64, 2, 2, 3, 64, 0},   // 3: wave 64x32
+    {64, 128, 2, 2, 3, 64, 0},   // 4: wave 32x64
+    {64, 64, 2, 2, 4, 64, 0},    // 5: wave 32x32, small M (batch-1 latency)
+    {32, 128, 1, 4, 4, 64, 0},   // 6: wave 32x32, very small M
+    {256, 256, 2, 4, 0, 64, 2},  // 7: 8 waves of 128x64, large M
+    {256, 128, 4, 2, 0, 64, 2},  // 8: 8 waves of 64x64
+    {128, 256, 2, 4, 0, 64, 2},  // 9: 8 waves of 64x64
+    {128, 64, 4, 1, 3, 64, 0},   // 10: wave 32x64, whole heads per wave for RoPE when N is not a multiple of 128
+    {256, 256, 2, 4, 0, 32, 4},  // 11: 8 waves of 128x64, 32-deep slabs, three in flight
+    {256, 128, 2, 2, 0, 32, 3},  // 12: 4 waves of 128x64, two workgroups per CU
+    {128, 256, 2, 2, 0, 32, 3},  // 13: 4 waves of 64x128, two workgroups per CU
 };
 constexpr int kTileCount = sizeof(kTiles) / sizeof(kTiles[0]);
 
-constexpr size_t lds_bytes(int bm, int bn) { return static_cast<size_t>(2) * (bm + bn) * BK * 2; }
+constexpr size_t lds_bytes(const TileDef& d) {
+  return d.pf ? static_cast<size_t>(2) * (d.bm + d.bn) * BK * 2 : static_cast<size_t>(d.st) * (d.bm + d.bn) * d.bk * 2;
+}
 
 template <typename T, Epi E>
 hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
   const TileDef& d = kTiles[tile];
   const dim3 grid(a.N / d.bn, (a.M + d.bm - 1) / d.bm, a.splits), block(d.threads());
-  const size_t lds = lds_bytes(d.bm, d.bn);
+  const size_t lds = lds_bytes(d);
   switch (tile) {
 #define LAYA_TILE(ID, BM_, BN_, WM_, WN_, PF_) \
   case ID: hipLaunchKernelGGL((gemm_kernel<T, BM_, BN_, WM_, WN_, PF_, E>), grid, block, lds, stream, a); break;
-    LAYA_TILE(0, 256, 256, 2, 2, 1)
-    LAYA_TILE(1, 256, 128, 2, 2, 1)
+#define LAYA_PIPE(ID, BM_, BN_, WM_, WN_, BK_, ST_) \
+  case ID: hipLaunchKernelGGL((gemm_pipe_kernel<T, BM_, BN_, WM_, WN_, BK_, ST_, E>), grid, block, lds, stream, a); break;
+    LAYA_PIPE(0, 256, 256, 2, 2, 64, 2)
+    LAYA_PIPE(1, 256, 128, 2, 2, 64, 2)
     LAYA_TILE(2, 128, 128, 2, 2, 2)
     LAYA_TILE(3, 128, 64, 2, 2, 3)
     LAYA_TILE(4, 64, 128, 2, 2, 3)
     LAYA_TILE(5, 64, 64, 2, 2, 4)
     LAYA_TILE(6, 32, 128, 1, 4, 4)
-    LAYA_TILE(7, 256, 256, 2, 4, 1)
-    LAYA_TILE(8, 256, 128, 4, 2, 1)
-    LAYA_TILE(9, 128, 256, 2, 4, 1)
+    LAYA_PIPE(7, 256, 256, 2, 4, 64, 2)
+    LAYA_PIPE(8, 256, 128, 4, 2, 64, 2)
+    LAYA_PIPE(9, 128, 256, 2, 4, 64, 2)
     LAYA_TILE(10, 128, 64, 4, 1, 3)
+    LAYA_PIPE(11, 256, 256, 2, 4, 32, 4)
+    LAYA_PIPE(12, 256, 128, 2, 2, 32, 3)
+    LAYA_PIPE(13, 128, 256, 2, 2, 32, 3)
 #undef LAYA_TILE
+#undef LAYA_PIPE
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -483,17 +684,19 @@ hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
 template <typename T, Epi E>
 hipError_t set_lds_attr() {
   hipError_t e = hipSuccess;
-#define LAYA_ATTR(BM_, BN_, WM_, WN_, PF_)                                                              \
+#define LAYA_ATTR(ID, ...)                                                                              \
   if (e == hipSuccess)                                                                                \
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<T, BM_, BN_, WM_, WN_, PF_, E>), \
-                            hipFuncAttributeMaxDynamicSharedMemorySize,                                 \
-                            static_cast<int>(lds_bytes(BM_, BN_)));
-  LAYA_ATTR(256, 256, 2, 2, 1)
-  LAYA_ATTR(256, 128, 2, 2, 1)
-  LAYA_ATTR(128, 128, 2, 2, 2)
-  LAYA_ATTR(256, 256, 2, 4, 1)
-  LAYA_ATTR(256, 128, 4, 2, 1)
-  LAYA_ATTR(128, 256, 2, 4, 1)
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&__VA_ARGS__),                                \
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_bytes(kTiles[ID])));
+  LAYA_ATTR(0, gemm_pipe_kernel<T, 256, 256, 2, 2, 64, 2, E>)
+  LAYA_ATTR(1, gemm_pipe_kernel<T, 256, 128, 2, 2, 64, 2, E>)
+  LAYA_ATTR(2, gemm_kernel<T, 128, 128, 2, 2, 2, E>)
+  LAYA_ATTR(7, gemm_pipe_kernel<T, 256, 256, 2, 4, 64, 2, E>)
+  LAYA_ATTR(8, gemm_pipe_kernel<T, 256, 128, 4, 2, 64, 2, E>)
+  LAYA_ATTR(9, gemm_pipe_kernel<T, 128, 256, 2, 4, 64, 2, E>)
+  LAYA_ATTR(11, gemm_pipe_kernel<T, 256, 256, 2, 4, 32, 4, E>)
+  LAYA_ATTR(12, gemm_pipe_kernel<T, 256, 128, 2, 2, 32, 3, E>)
+  LAYA_ATTR(13, gemm_pipe_kernel<T, 128, 256, 2, 2, 32, 3, E>)
 #undef LAYA_ATTR
   return e;
 }

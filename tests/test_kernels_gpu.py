@@ -164,8 +164,11 @@ def linear(x, w, bias, out, kind, dtype, M, N, K, splits, tile):
     sync()
 
 
+GEMM_TILES = 14  # tile ids of laya_op_linear (csrc/gemm.hip kTiles)
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("tile", range(11))
+@pytest.mark.parametrize("tile", range(GEMM_TILES))
 def test_linear_tiles_match_fp32_product(gpu, dtype, tile):
     t = torch()
     rng = np.random.default_rng(tile)
@@ -178,15 +181,16 @@ def test_linear_tiles_match_fp32_product(gpu, dtype, tile):
                                    atol=1e-4, rtol=1e-4)
 
 
+@pytest.mark.parametrize("tile", [5, 11, 12])
 @pytest.mark.parametrize("splits", [2, 3, 4])
-def test_linear_split_k_partials_sum_to_the_product(gpu, splits):
+def test_linear_split_k_partials_sum_to_the_product(gpu, splits, tile):
     t = torch()
     rng = np.random.default_rng(splits)
     M, N, K = 64, 768, 3072
     x = half_round(rng.normal(0, 1, (M, K)), "f16")
     w = half_round(rng.normal(0, 1 / math.sqrt(K), (N, K)), "f16")
     out = t.full((splits, M, N), float("nan"), device=gpu)
-    linear(to16(x, "f16", gpu), to16(w, "f16", gpu), None, out, 0, "f16", M, N, K, splits, 5)
+    linear(to16(x, "f16", gpu), to16(w, "f16", gpu), None, out, 0, "f16", M, N, K, splits, tile)
     np.testing.assert_allclose(out.sum(0).cpu().numpy(), x.astype(np.float64) @ w.T.astype(np.float64),
                                atol=1e-4, rtol=1e-4)
 
@@ -221,7 +225,7 @@ def test_linear_gelu_epilogue(gpu, dtype):
     np.testing.assert_allclose(from16(out), expected, atol=tol, rtol=tol)
 
 
-@pytest.mark.parametrize("tile", [0, 2, 5, 6, 7, 9])
+@pytest.mark.parametrize("tile", [0, 2, 5, 6, 7, 9, 11, 12, 13])
 def test_qkv_epilogue_writes_head_major_layout(gpu, tile):
     """Integer-valued operands make the product exact, so the layout check is bit-exact."""
     t = torch()
@@ -343,7 +347,8 @@ def test_linear_geglu_epilogue_on_interleaved_rows(gpu, dtype, tile):
     np.testing.assert_allclose(from16(out), expected, atol=tol, rtol=tol)
 
 
-@pytest.mark.parametrize("tile,heads", [(-1, 4), (2, 4), (4, 4), (7, 4), (10, 4), (-1, 3), (10, 3), (-1, 1)])
+@pytest.mark.parametrize("tile,heads", [(-1, 4), (2, 4), (4, 4), (7, 4), (10, 4), (11, 4), (12, 4), (13, 4), (-1, 3), (10, 3),
+                                        (-1, 1)])
 def test_qkv_epilogue_applies_rope_to_q_and_k(gpu, tile, heads):
     """RoPE in fp32 before the single rounding, matching the oracle's rotate-half on the same rows;
     odd head counts (3 * width not a multiple of 128) take the 128x64 tile."""
