@@ -25,6 +25,13 @@ namespace {
 
 constexpr int KB = 64;  // keys per block
 
+// LDS rows of K and V^T blocks are 128 B (64 16-bit values) as eight 16-byte chunks, the chunk index
+// XOR-swizzled by (row / 2) % 8: a 16-byte LDS read is served 16 lanes per pass from 64 banks, the
+// lanes of a pass read one chunk position of 16 consecutive rows (eight 256-byte row pairs), and
+// the swizzle spreads those pairs over the eight chunk positions (row % 8 would put rows 8 apart on
+// the same banks).
+__device__ __forceinline__ int kvswz(int row) { return (row >> 1) & 7; }
+
 // One 64-key block of the single-pass softmax for this lane's query q.  s holds the raw QK^T
 // scores of keys kb + 32kt + 8(r/4) + 4g + r%4 (the S^T accumulator layout); the reference max
 // `mrow` is kept in the scaled log2 domain (x * log2(e) / 8), so each probability costs one FMA
@@ -103,7 +110,7 @@ __device__ __forceinline__ void work_item(int nx, int ny, int* tile, int* head) 
 
 // One 64-key block of K and V^T moved from HBM to LDS by NTH cooperating threads: global loads
 // are row-contiguous 16-byte chunks (8 lanes per 128-byte row), LDS rows are 128 bytes with the
-// chunk index XOR-swizzled by (row & 7).  V^T rows store keys permuted within each 16-key group
+// chunk index XOR-swizzled by kvswz(row).  V^T rows store keys permuted within each 16-key group
 // (logical keys 4g..4g+3 and 8+4g..8+4g+3 at physical 8g..8g+7) so that a lane's 16-byte read is
 // exactly the eight keys whose probabilities the S^T accumulator leaves in that lane.
 template <typename T, int NTH>
@@ -129,10 +136,10 @@ struct KVStage {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + NTH * i, r = c >> 3, u = c & 7;
-      *reinterpret_cast<i32x4*>(sK + r * 64 + ((u ^ (r & 7)) << 3)) = rk[i];
+      *reinterpret_cast<i32x4*>(sK + r * 64 + ((u ^ kvswz(r)) << 3)) = rk[i];
       const int cg = u >> 1, half = u & 1;  // keys 8u..8u+7 = half `half` of 16-key group cg
       T* vrow = sV + r * KB;
-      const int p0 = ((2 * cg) ^ (r & 7)) << 3, p1 = ((2 * cg + 1) ^ (r & 7)) << 3;
+      const int p0 = ((2 * cg) ^ kvswz(r)) << 3, p1 = ((2 * cg + 1) ^ kvswz(r)) << 3;
       *reinterpret_cast<int2*>(vrow + p0 + 4 * half) = make_int2(rv[i][0], rv[i][1]);
       *reinterpret_cast<int2*>(vrow + p1 + 4 * half) = make_int2(rv[i][2], rv[i][3]);
     }
@@ -157,7 +164,7 @@ __device__ __forceinline__ void attend_block(const T* sK, const T* sV, const typ
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int ch = 2 * ks + g;
-      const T8 kf = *reinterpret_cast<const T8*>(sK + kr * 64 + ((ch ^ (kr & 7)) << 3));
+      const T8 kf = *reinterpret_cast<const T8*>(sK + kr * 64 + ((ch ^ kvswz(kr)) << 3));
       s[kt] = mfma32(kf, qf[ks], s[kt]);
     }
   }
@@ -170,7 +177,7 @@ __device__ __forceinline__ void attend_block(const T* sK, const T* sV, const typ
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
       const int vr = d * 32 + ql;
-      const T8 vf = *reinterpret_cast<const T8*>(sV + vr * KB + (((2 * c + g) ^ (vr & 7)) << 3));
+      const T8 vf = *reinterpret_cast<const T8*>(sV + vr * KB + (((2 * c + g) ^ kvswz(vr)) << 3));
       o[d] = mfma32(vf, pb, o[d]);
     }
   }

@@ -470,7 +470,6 @@ void gemm_pipe_kernel(GemmArgs a) {
   constexpr int kWaitAll = 7 << 4;
   typedef typename Vec8<T>::type T8;
   typedef __attribute__((address_space(3))) void* LdsPtr;
-  typedef __attribute__((address_space(1))) void* GlobalPtr;
 
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* const lds = reinterpret_cast<T*>(smem_raw);

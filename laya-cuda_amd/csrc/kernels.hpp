@@ -38,6 +38,7 @@ struct AddNormArgs {
   int rows;
   const float* row_table;    // [n][d] rows added per token (question types), or null
   const int32_t* row_index;  // [rows] row of row_table for each token
+  const void* branch16;      // [rows][d] 16-bit branch (bias already added), instead of parts, or null
 };
 
 bool norm_width_supported(int width);

@@ -70,6 +70,13 @@ __global__ __launch_bounds__(256) void add_norm_kernel(AddNormArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < D / 64; ++i) v[i] = v[i] + br[i];
+  } else if (a.branch16) {
+    // 16-bit projection output with its bias already added before rounding (the reference's
+    // layer_norm adds a half branch to the fp32 residual, kernels.cu:20-35).
+    float br[D / 64];
+    load_row16<D, T>(static_cast<const T*>(a.branch16) + off, lane, br);
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) v[i] = v[i] + br[i];
   }
   if (a.row_table) {  // question-type row of this token (type_add, kernels.cu:155-158)
     float t[D / 64];

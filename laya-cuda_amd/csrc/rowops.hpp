@@ -62,6 +62,22 @@ __device__ __forceinline__ void store_row16(T* dst, int lane, const float (&v)[D
   }
 }
 
+template <int D, typename T>
+__device__ __forceinline__ void load_row16(const T* src, int lane, float (&v)[D / 64]) {
+  using R = RowMap<D>;
+#pragma unroll
+  for (int c = 0; c < R::C; ++c) {
+    if constexpr (R::V == 4) {
+      const typename Vec4<T>::type t = *reinterpret_cast<const typename Vec4<T>::type*>(src + R::index(c, lane, 0));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[c * 4 + i] = to_float<T>(t[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < R::V; ++i) v[c * R::V + i] = to_float<T>(src[R::index(c, lane, i)]);
+    }
+  }
+}
+
 // LayerNorm parameters of a row, loaded into registers at kernel start so that their latency
 // overlaps the row's own loads instead of following the reductions.
 template <int D> struct NormParams {

@@ -157,6 +157,10 @@ struct Slot {
   void *attn_sel = nullptr, *x_sel = nullptr, *ff_sel = nullptr;
   float* part_sel = nullptr;
   int tile[4] = {0, 0, 0, 0}, splits[4] = {1, 1, 1, 1};  // qkv, o, up, down
+  // Batched slots store the out and down projections as 16-bit rows with the bias added before
+  // the rounding (the reference's branch buffer, runtime.py:70-75 with kernels.cu:20-35 and
+  // 50-55); batch-1 slots keep fp32 split-K partials, summed with the bias in the norm kernel.
+  bool branch16 = false;
   // Head transformer layers: in_proj, out_proj, linear1, linear2 over all rows, then out_proj,
   // linear1, linear2 over the readout rows.
   int htile[7] = {0, 0, 0, 0, 0, 0, 0}, hsplits[7] = {1, 1, 1, 1, 1, 1, 1};
@@ -327,6 +331,11 @@ void destroy_slot(Engine& E, Slot* s) {
   delete s;
 }
 
+// Packed rows from which a slot keeps the projection outputs that feed a residual add in 16 bits:
+// there the GEMMs need no split-K and the fp32 partials would be the largest HBM stream of the
+// add+LayerNorm kernels.
+constexpr int kBranch16Rows = 4096;
+
 Slot* create_slot(Engine& E, int m, int b, int k) {
   const LayaConfig& c = E.cfg;
   Slot* s = new Slot();
@@ -346,6 +355,12 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
     }
     gemm_plan(m, d, f, Epi::F32, E.mfma(), E.cus, &s->tile[3], &s->splits[3]);
     s->splits[0] = s->splits[2] = 1;
+    if (m >= kBranch16Rows) {
+      s->branch16 = true;
+      gemm_plan(m, d, d, Epi::HALF, E.mfma(), E.cus, &s->tile[1], &s->splits[1]);
+      gemm_plan(m, d, f, Epi::HALF, E.mfma(), E.cus, &s->tile[3], &s->splits[3]);
+      s->splits[1] = s->splits[3] = 1;
+    }
     if (E.modern) {  // head transformer layers: all rows, then the readout rows of the last one
       gemm_plan(m, 3 * d, d, Epi::QKV, E.mfma(), E.cus, &s->htile[0], &s->hsplits[0]);
       gemm_plan(m, d, d, Epi::F32, E.mfma(), E.cus, &s->htile[1], &s->hsplits[1]);
@@ -502,6 +517,16 @@ bool stage_used(const Engine& E, int stage, int layer) {
   return stage >= 0 && stage < kStageCount;
 }
 
+// Batched slots: the norm after the out/down projection adds their 16-bit output (bias included)
+// instead of summing fp32 partials and the bias.
+void use_branch16(const Slot& s, AddNormArgs& na) {
+  if (!s.branch16) return;
+  na.branch16 = na.parts;
+  na.parts = nullptr;
+  na.splits = 1;
+  na.bias = nullptr;
+}
+
 void launch_stage(Engine& E, Slot& s, int stage, int layer) {
   const LayaConfig& c = E.cfg;
   const int m = s.m, d = c.width, f = c.intermediate, R = s.L.R;
@@ -542,7 +567,8 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
     case kAttnOut:
       g.a = s.attn; g.b = ly->wo; g.M = m; g.N = d; g.K = d; g.lda = d; g.ldb = d;
       g.out = s.part; g.ldo = d; g.split_stride = md; g.splits = s.splits[1];
-      check_launch(launch_gemm(g, Epi::F32, t, s.tile[1], st), "attn out");
+      if (s.branch16) g.bias = ly->bo;  // null for ModernBERT
+      check_launch(launch_gemm(g, s.branch16 ? Epi::HALF : Epi::F32, t, s.tile[1], st), "attn out");
       break;
     case kAttnNorm: {
       // BERT-style: residual = LN(residual + branch + bias).  ModernBERT (pre-LN):
@@ -550,6 +576,7 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       AddNormArgs na = E.modern
           ? AddNormArgs{s.residual, s.part, s.splits[1], md, nullptr, ly->n2g, nullptr, c.eps, s.residual, nullptr, s.x, m}
           : AddNormArgs{s.residual, s.part, s.splits[1], md, ly->bo, ly->n1g, ly->n1b, c.eps, nullptr, s.residual, s.x, m};
+      use_branch16(s, na);
       check_launch(launch_add_norm(na, d, t, st), "attention norm");
       break;
     }
@@ -562,7 +589,8 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
     case kFfnDown:
       g.a = s.ff; g.b = ly->wo2; g.M = m; g.N = d; g.K = f; g.lda = f; g.ldb = f;
       g.out = s.part; g.ldo = d; g.split_stride = md; g.splits = s.splits[3];
-      check_launch(launch_gemm(g, Epi::F32, t, s.tile[3], st), "ffn down");
+      if (s.branch16) g.bias = ly->bo2;  // null for ModernBERT
+      check_launch(launch_gemm(g, s.branch16 ? Epi::HALF : Epi::F32, t, s.tile[3], st), "ffn down");
       break;
     case kFfnNorm: {
       AddNormArgs na{};
@@ -575,6 +603,7 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
         na = AddNormArgs{s.residual, s.part, s.splits[3], md, nullptr, E.final_norm, nullptr, c.eps, nullptr,
                          s.residual, nullptr, m};
       }
+      use_branch16(s, na);
       check_launch(launch_add_norm(na, d, t, st), "ffn norm");
       break;
     }

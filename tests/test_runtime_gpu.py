@@ -109,6 +109,30 @@ def test_ragged_batch_matches_oracle(gpu):
         rt.close()
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_batched_encoder_matches_oracle(gpu, dtype):
+    """A batched slot (more than 4,096 packed rows): the large-tile GEMM pipeline and the 16-bit
+    out/down projection rows with their bias added before rounding, as the reference's branch
+    buffer.  Tolerances as for the batch-1 workloads (fp16 1e-3, bf16 2e-3)."""
+    spec = synthetic.adapter(None, layers=2, width=256, heads=4, intermediate=1024, vocab=3000, positions=1024,
+                             max_len=1024, mfma_dtype=dtype)
+    w = synthetic.weights(spec, seed=3)
+    rng = np.random.default_rng(5)
+    lengths = rng.integers(300, 1000, 9)
+    sequences = [rng.integers(5, 3000, int(n), dtype=np.int32) for n in lengths]
+    questions = [(i, sorted(rng.choice(np.arange(1, int(n)), 5, replace=False).tolist()), i % 3)
+                 for i, n in enumerate(lengths)]
+    want, want_acts = oracle_logits(spec, w, sequences, questions)
+    rt = Runtime(spec, 0, 2, weights=w)
+    try:
+        logits, acts, metrics = rt.predict_sequences(sequences, questions)
+        assert metrics["shape"][0] >= 4096, metrics["shape"]
+        worst = compare(logits, acts, want, want_acts, atol=LOGIT_ATOL if dtype == "float16" else 2e-3)
+        print(f"batched {dtype}: rows {metrics['shape'][0]}, max |logit error| = {worst:.3e}")
+    finally:
+        rt.close()
+
+
 def test_reference_items_each_question_its_own_row(gpu):
     """Runtime.predict(items) packs every question as its own sequence (runtime.py:52-68)."""
     spec = synthetic.adapter(None, layers=2, width=128, heads=2, intermediate=512, vocab=1000, positions=64,
