@@ -32,6 +32,27 @@ constexpr int KB = 64;  // keys per block
 // the same banks).
 __device__ __forceinline__ int kvswz(int row) { return (row >> 1) & 7; }
 
+// Combine a value with the one held by lane l ^ 32 (the other half of the S^T accumulator's k-slots
+// for the same query) with v_permlane32_swap: a VALU lane exchange, no LDS round trip.
+__device__ __forceinline__ float half_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// acc + p.x + p.y for two 16-bit probabilities, in fp32 (v_dot2_f32_{f16,bf16} against (1, 1)).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float sum2(f16x2 p, float acc) {
+  return __builtin_amdgcn_fdot2(p, f16x2{1.0f16, 1.0f16}, acc, false);
+}
+__device__ __forceinline__ float sum2(bf16x2 p, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(p, bf16x2{static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)}, acc, false);
+}
+
 // One 64-key block of the single-pass softmax for this lane's query q.  s holds the raw QK^T
 // scores of keys kb + 32kt + 8(r/4) + 4g + r%4 (the S^T accumulator layout); the reference max
 // `mrow` is kept in the scaled log2 domain (x * log2(e) / 8), so each probability costs one FMA
@@ -41,11 +62,13 @@ __device__ __forceinline__ int kvswz(int row) { return (row >> 1) & 7; }
 // branch.
 //
 // The reference max only moves when a block's max exceeds it by more than 8 (so probabilities
-// stay <= 2^8: exact enough as 16-bit MFMA operands, summed in fp32), and the O/lsum rescale runs
-// only when some lane of the wave moved it: after the first blocks most blocks skip it.  The
-// normaliser uses the same reference as the numerators, so the result is the softmax either way.
-// A block whose keys are all masked for this query leaves its state untouched.  On return s holds
-// the block's unnormalised probabilities, lsum and o are rescaled.
+// stay <= 2^8: exact enough as 16-bit MFMA operands), and the O/lsum rescale runs only when some
+// lane of the wave moved it: after the first blocks most blocks skip it.  The normaliser uses the
+// same reference as the numerators, so the result is the softmax either way.  A block whose keys
+// are all masked for this query leaves its state untouched.  On return s holds the block's
+// unnormalised probabilities and lsum and o are rescaled; the caller adds the block's probabilities
+// to lsum as it rounds them to the 16-bit MFMA operands (so the weights that multiply V are the
+// ones the normaliser sums).
 __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], float& mrow, float& lsum, int kb,
                                               bool edge, int qlo, int qhi, int g) {
   constexpr float c = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) in the exp2 domain
@@ -66,7 +89,7 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], fl
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx[r & 3] = fmaxf(mx[r & 3], s[kt][r]);
   float bmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
-  bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64)) * c;
+  bmax = half_max(bmax) * c;
   const bool grow = bmax > mrow + kSlack;  // false while everything seen so far is masked
   if (__builtin_amdgcn_ballot_w64(grow)) {
     // Lanes that keep their reference (including ones that have seen only masked keys) scale by 1;
@@ -80,16 +103,11 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], fl
       for (int r = 0; r < 16; ++r) o[d][r] *= alpha;
   }
   const float base = mrow == -INFINITY ? 0.f : mrow;  // nothing seen yet: probabilities are 0
-  float part[4] = {0.f, 0.f, 0.f, 0.f};                // four independent sums: a short dependency chain
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], c, -base));  // masked: exp2(-inf) = 0
-      s[kt][r] = p;
-      part[r & 3] += p;
-    }
-  lsum += (part[0] + part[1]) + (part[2] + part[3]);
+    for (int r = 0; r < 16; ++r)
+      s[kt][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], c, -base));  // masked: exp2(-inf) = 0
 }
 
 // Workgroup -> (tile, head).  Workgroups are dealt to the 8 XCDs round-robin by linear id; when the
@@ -169,11 +187,16 @@ __device__ __forceinline__ void attend_block(const T* sK, const T* sV, const typ
     }
   }
   softmax_block(s, o, mrow, lsum, kb, edge, qlo, qhi, g);
+  float rs[2] = {0.f, 0.f};  // two short dependency chains of row-sum dot products
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     T8 pb;
 #pragma unroll
     for (int e = 0; e < 8; ++e) pb[e] = to_half<T>(s[c >> 1][8 * (c & 1) + e]);
+    rs[0] = sum2(__builtin_shufflevector(pb, pb, 0, 1), rs[0]);
+    rs[1] = sum2(__builtin_shufflevector(pb, pb, 2, 3), rs[1]);
+    rs[0] = sum2(__builtin_shufflevector(pb, pb, 4, 5), rs[0]);
+    rs[1] = sum2(__builtin_shufflevector(pb, pb, 6, 7), rs[1]);
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
       const int vr = d * 32 + ql;
@@ -181,6 +204,7 @@ __device__ __forceinline__ void attend_block(const T* sK, const T* sV, const typ
       o[d] = mfma32(vf, pb, o[d]);
     }
   }
+  lsum += rs[0] + rs[1];
 }
 
 // Rows of no sequence (span padding, rows past the last sequence) are exact zeros (kernels.cu:102).
@@ -271,7 +295,7 @@ __device__ __forceinline__ void attention_shared(const AttnArgs& a) {
   }
 
   if (!qin) return;
-  const float total = lsum + __shfl_xor(lsum, 32, 64);
+  const float total = half_sum(lsum);
   const float inv = qvalid ? 1.0f / total : 0.f;
   T* orow = out + static_cast<size_t>(q) * ld + head * 64;
 #pragma unroll
@@ -365,7 +389,7 @@ __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
   // Merge the waves' partial results: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w.
   __syncthreads();  // every wave is done with the staging area
   float* sO = reinterpret_cast<float*>(lds) + wave * 32 * OP;
-  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  const float ltot = half_sum(lsum);
   if (g == 0) {
     sM[wave][ql] = mrow;
     sL[wave][ql] = ltot;

@@ -67,20 +67,22 @@ __device__ __forceinline__ float gelu(float v) { return 0.5f * v * (1.0f + erff(
 // from Abramowitz & Stegun, Handbook of Mathematical Functions, formula 7.1.26:
 //   erfc(z) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2),  t = 1 / (1 + p z),  z >= 0,
 // absolute error <= 1.5e-7 (far below the 2^-11 relative rounding of fp16 that follows).
-// GELU(x) = x Phi(x) with Phi(x) = 1 - erfc(z)/2 for x >= 0 and erfc(z)/2 for x < 0, z = |x|/sqrt(2),
-// so large negative inputs never subtract nearly equal numbers.  One reciprocal and one exp2 per
-// element instead of the libm erff's range reduction: the epilogue of a 65536 x 4096 GEMM runs
+// With q = Phi(-|x|) = erfc(|x|/sqrt(2))/2, GELU(x) = x Phi(x) is x (1 - q) for x >= 0 and x q for
+// x < 0, i.e. max(x, 0) - |x| q: one max and one FMA instead of a compare, a select and two
+// products, and large negative inputs never subtract nearly equal numbers.  The 1/sqrt(2) is folded
+// into p and the 1/2 into the a_i, so a value costs one reciprocal, one exp2 and nine VALU
+// operations instead of the libm erff's range reduction: the epilogue of a 65536 x 4096 GEMM runs
 // this 268M times.
 __device__ __forceinline__ float gelu16(float x) {
-  const float z = fabsf(x) * 0.7071067811865475f;
-  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, z, 1.0f));
-  float poly = __builtin_fmaf(t, 1.061405429f, -1.453152027f);
-  poly = __builtin_fmaf(t, poly, 1.421413741f);
-  poly = __builtin_fmaf(t, poly, -0.284496736f);
-  poly = __builtin_fmaf(t, poly, 0.254829592f);
-  const float erfc = t * poly * __builtin_amdgcn_exp2f(-z * z * 1.4426950408889634f);
-  const float phi = x >= 0.f ? 1.0f - 0.5f * erfc : 0.5f * erfc;
-  return x * phi;
+  const float ax = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f * 0.7071067811865475f, ax, 1.0f));
+  float poly = __builtin_fmaf(t, 0.5f * 1.061405429f, 0.5f * -1.453152027f);
+  poly = __builtin_fmaf(t, poly, 0.5f * 1.421413741f);
+  poly = __builtin_fmaf(t, poly, 0.5f * -0.284496736f);
+  poly = __builtin_fmaf(t, poly, 0.5f * 0.254829592f);
+  // exp(-z^2) = exp2(-x^2 log2(e) / 2)
+  const float q = t * poly * __builtin_amdgcn_exp2f(x * x * (-0.5f * 1.4426950408889634f));
+  return __builtin_fmaf(-ax, q, fmaxf(x, 0.f));
 }
 
 }  // namespace laya

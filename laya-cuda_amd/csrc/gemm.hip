@@ -514,12 +514,13 @@ void gemm_pipe_kernel(GemmArgs a) {
   // reads before every load and serialises the fragment reads of the next k-step with the MFMAs.
   // Here the stage a load writes is never read until after a barrier that follows an explicit
   // s_waitcnt on those loads, so no such wait is needed.  M0 holds the LDS destination of the
-  // instruction (one s_nop after writing it before the LDS DMA reads it).
+  // instruction (bound through the {m0} operand constraint, so the compiler writes it and knows it
+  // is live; one s_nop between that write and the LDS DMA that reads it).
   const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>((LdsPtr)smem_raw));
   auto issue = [&](int q, int kt, int st) {
     const T* g = src[q] + static_cast<size_t>(kt) * BKS;
     const unsigned m0 = lds_base + static_cast<unsigned>(st * SLAB + dst[q]) * 2;
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0));
   };
 
   f32x16 acc[TM][TN];
