@@ -23,7 +23,8 @@ Fields:
 ``--calibrate-copy`` first runs a 64 MiB device copy (the reference for the HBM byte counters of a
 ``rocprofv3 --pmc`` run).  ``--eager`` launches the forward kernel by kernel instead of replaying its hipGraph (for
 profilers that cannot follow graph launches).  ``--extras`` adds the other workloads: 83- and 1,024-token latency, the 32-request ragged batch
-(sequences/s) and the 24-layer d=1024 64 x 1024 batch (sequences/s and MFMA utilisation).
+(sequences/s) and the 24-layer d=1024 64 x 1024 batch (sequences/s and MFMA utilisation);
+``--workloads`` picks a subset of them.
 """
 import argparse
 import json
@@ -219,8 +220,11 @@ def run_extras(args):
     from laya_cuda.runtime import Runtime
 
     extras = {}
+    chosen = args.workloads.split(",") if args.workloads else None
     for name, dtype in (("l83", "float16"), ("l1024", "float16"), ("ragged32", "float16"),
                         ("b64x1024", "bfloat16")):
+        if chosen and name not in chosen:
+            continue
         spec = synthetic.adapter(name, mfma_dtype=dtype)
         weights = synthetic.weights(spec, seed=0, bf16=synthetic.WORKLOADS[name].get("bf16", False))
         sequences, questions = synthetic.request(name, seed=1)
@@ -350,6 +354,8 @@ def main():
     ap.add_argument("--batching", action="store_true",
                     help="with --extras: serialized Engine vs BatchEngine under 1/8/32 outstanding requests")
     ap.add_argument("--batching-samples", type=int, default=100)
+    ap.add_argument("--workloads", default="",
+                    help="with --extras: comma-separated subset of l83,l1024,ragged32,b64x1024 (default all)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the encoder path shards by request with no collective, and "
