@@ -176,15 +176,16 @@ int laya_op_norm(float* residual, const float* branch, int splits, int64_t part_
  * out[M][N] = x[M][K] w[N][K]^T (+ bias).  kind 0: fp32 out (split-K partials at out + z*M*N when
  * splits > 1, bias then must be NULL), 1: 16-bit out, 2: 16-bit exact-GELU out, 3: 16-bit ReLU out,
  * 4: GeGLU, out[M][N/2] = gelu(gate) * value with w's rows in the resident GeGLU interleave
- * (32-row groups: 16 gate rows, then their 16 value rows).  tile < 0 lets the planner choose tile
- * and splits (splits ignored). */
+ * (32-row groups: 16 gate rows, then their 16 value rows).  tile -1 lets the planner choose tile
+ * and splits (splits ignored): the measured plan table when it holds the problem, else the
+ * heuristic; tile -2 takes the heuristic alone (the baseline the plan table is measured against). */
 int laya_op_linear(const void* x, const void* w, const float* bias, void* out, int kind,
                    int dtype16, int M, int N, int K, int splits, int tile, void* stream);
 
 /* QKV projection with the head-major epilogue that replaces `layout` (kernels.cu:68-82):
  * q, k [heads][M][64], vt [heads][64][M].  With rope_cos non-NULL, Q and K are rotated (rotate-half
  * RoPE, kernels.cu:73-77) in fp32 before rounding, by the [positions][32] cos/sin tables at each
- * row's positions[row].  M must be a multiple of 8. */
+ * row's positions[row].  M must be a multiple of 8.  tile -1 / -2 as for laya_op_linear. */
 int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* k, void* vt,
                 const float* rope_cos, const float* rope_sin, const int32_t* positions, int dtype16,
                 int M, int width, int tile, void* stream);

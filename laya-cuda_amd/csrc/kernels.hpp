@@ -75,9 +75,11 @@ struct GemmTile {
 };
 int gemm_tile_count();
 GemmTile gemm_tile(int id);
-// Chooses a tile and split count for a problem on `cus` compute units.
+// Chooses a tile and split count for a problem on `cus` compute units: the measured plan table
+// (gemm_plans.inc) when it has the problem and `measured`, else the heuristic.
 // rope: the QKV epilogue applies RoPE, which needs wave tiles of 64-column multiples.
-void gemm_plan(int M, int N, int K, Epi epi, DType t, int cus, int* tile, int* splits, bool rope = false);
+void gemm_plan(int M, int N, int K, Epi epi, DType t, int cus, int* tile, int* splits, bool rope = false,
+               bool measured = true);
 hipError_t gemm_prepare();  // sets LDS attributes of the large-tile kernels (call once per device)
 hipError_t launch_gemm(const GemmArgs& a, Epi epi, DType t, int tile, hipStream_t stream);
 

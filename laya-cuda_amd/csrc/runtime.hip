@@ -1243,7 +1243,7 @@ int laya_op_linear(const void* x, const void* w, const float* bias, void* out, i
                                                                                                     : Epi::GEGLU;
     int cus = 256;
     if (tile < 0) {
-      gemm_plan(M, N, K, epi, half_type(dtype16), cus, &tile, &splits);
+      gemm_plan(M, N, K, epi, half_type(dtype16), cus, &tile, &splits, false, tile == -1);
       if (bias) splits = 1;
     }
     LAYA_REQUIRE(tile < gemm_tile_count(), "bad tile id");
@@ -1264,7 +1264,7 @@ int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* 
     int splits = 1;
     const bool rope = rope_cos != nullptr;
     LAYA_REQUIRE(!rope || (rope_sin && positions), "RoPE needs cos, sin and positions");
-    if (tile < 0) gemm_plan(M, 3 * width, width, Epi::QKV, half_type(dtype16), 256, &tile, &splits, rope);
+    if (tile < 0) gemm_plan(M, 3 * width, width, Epi::QKV, half_type(dtype16), 256, &tile, &splits, rope, tile == -1);
     LAYA_REQUIRE(tile < gemm_tile_count(), "bad tile id");
     LAYA_REQUIRE(width % 64 == 0 && (3 * width) % gemm_tile(tile).bn == 0, "width does not fit the tile");
     LAYA_REQUIRE(M % 8 == 0, "rows must be a multiple of 8 (V^T is stored in runs of 8 tokens)");

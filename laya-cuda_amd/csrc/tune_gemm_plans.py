@@ -3,7 +3,7 @@
 For every encoder shape family below, every packed-row class up to 2,048 rows (the classes
 laya_cuda.runtime rounds requests to) and both MFMA input types, each GEMM of the forward is timed
 through the op-level C ABI (laya_op_linear / laya_op_qkv) with every tile id and, for the fp32
-split-K epilogue, 1/2/4/8 splits, and also with the library's own heuristic plan (tile -1).  A
+split-K epilogue, 1/2/4/8 splits, and also with the library's own heuristic plan (tile -2).  A
 problem gets a table row only when the best measured launch beats the heuristic by more than 3%;
 the library looks rows up at slot creation (exact match on CUs, M, N, K, epilogue, type, RoPE).
 
@@ -103,9 +103,9 @@ def main():
                                                            lib_dtype, M, N // 3, tile, stream)
                         return lambda: lib.laya_op_linear(p(x), p(w), None, p(out), KIND[epi], lib_dtype, M, N, K,
                                                           splits, tile, stream)
-                    heuristic = timed(launch(-1, 1))
+                    heuristic = timed(launch(-2, 1))
                     best = None
-                    for tile in range(16):
+                    for tile in range(24):
                         for splits in ((1, 2, 4, 8) if epi == F32 else (1,)):
                             if splits > 1 and K // 64 // splits < 2:
                                 continue
