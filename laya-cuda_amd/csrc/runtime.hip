@@ -377,10 +377,12 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
       s->attn_mode = kAttnSharedKV;
       s->attn_waves = 8;
     } else {
-      // Two waves per 32-query tile: measured faster than four at 512 and 1,024 keys (the extra
-      // waves cost more in LDS staging and merging than they save in serial key blocks).
+      // Each 32-query tile's keys split across waves.  Four waves halve the serial key blocks per
+      // wave but take 128 KB of LDS, one workgroup per CU: measured 6.7 against 9.1 us at 512
+      // tokens (192 workgroups, one round), while at 1,024 tokens (384 workgroups) two waves, two
+      // workgroups per CU and one round win, 16.3 against 18.4 us.
       s->attn_mode = kAttnSplitKeys;
-      s->attn_waves = 2;
+      s->attn_waves = static_cast<long long>((m + 31) / 32) * c.heads <= E.cus ? 4 : 2;
     }
     // Tiles of at most `block` rows: every sequence, and every run of rows between or after
     // sequences, adds at most one partial tile, so this bounds the work list of any request.
