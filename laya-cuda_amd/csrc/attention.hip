@@ -322,15 +322,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void a
 // Small batches (few query tiles): a workgroup owns 32 queries of one sequence and one head, and
 // its NW waves split that sequence's 64-key blocks (wave w takes blocks w, w+NW, ...), so the
 // serial chain per wave is ceil(blocks / NW) instead of blocks.  Each wave stages its own blocks
-// through its own double-buffered LDS region with coalesced loads (the next one in flight while
-// it computes the current one); the NW partial (max, sum, O) triples are merged through LDS.
+// through its own LDS region with coalesced loads (the next block in flight in registers while it
+// computes the current one; one region suffices, since a wave's LDS accesses execute in issue
+// order, and 16 KB per wave lets two four-wave workgroups share a CU); the NW partial (max, sum, O)
+// triples are merged through LDS.
 template <typename T, int NW>
 __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
   typedef typename Vec8<T>::type T8;
   typedef typename Vec4<T>::type T4;
   constexpr int NT = 64 * NW;
   constexpr int OP = 65;  // LDS pitch of a merged query row (floats): conflict-free column writes
-  constexpr int STAGE = 2 * 2 * KB * 64;  // per wave: two buffers of K and V^T (16-bit elements)
+  constexpr int STAGE = 2 * KB * 64;  // per wave: one K block and one V^T block (16-bit elements)
 
   int tile, head;
   work_item(a.max_tiles, a.heads, &tile, &head);
@@ -378,9 +380,9 @@ __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
   const int qlo = local ? max(start, q - a.window) : start;
   const int qhi = local ? max(qlo, min(kend, q + a.window + 1)) : kend;
   if (wave < nkb) st.load(K, Vt, a.m, klo + KB * wave, lane);
-  for (int j = wave, it = 0; j < nkb; j += NW, ++it) {
-    T* sK = mine + (it & 1) * 2 * KB * 64;
-    T* sV = sK + KB * 64;
+  T* const sK = mine;
+  T* const sV = mine + KB * 64;
+  for (int j = wave; j < nkb; j += NW) {
     st.store(sK, sV, lane);
     if (j + NW < nkb) st.load(K, Vt, a.m, klo + KB * (j + NW), lane);
     attend_block<T>(sK, sV, qf, o, mrow, lsum, klo + KB * j, local || klo + KB * (j + 1) > kend, qlo, qhi, lane);

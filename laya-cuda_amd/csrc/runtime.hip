@@ -378,9 +378,10 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
       s->attn_waves = 8;
     } else {
       // Each 32-query tile's keys split across waves.  Four waves halve the serial key blocks per
-      // wave but take 128 KB of LDS, one workgroup per CU: measured 6.7 against 9.1 us at 512
-      // tokens (192 workgroups, one round), while at 1,024 tokens (384 workgroups) two waves, two
-      // workgroups per CU and one round win, 16.3 against 18.4 us.
+      // wave, but the kernel's registers (one wave per SIMD) leave room for one such workgroup per
+      // CU: measured 6.6 against 8.7 us at 512 tokens (192 workgroups, one round), while at 1,024
+      // tokens (384 workgroups) two waves, two workgroups per CU and one round win, 15.9 against
+      // 17.8 us.
       s->attn_mode = kAttnSplitKeys;
       s->attn_waves = static_cast<long long>((m + 31) / 32) * c.heads <= E.cus ? 4 : 2;
     }
