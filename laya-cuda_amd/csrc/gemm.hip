@@ -441,6 +441,9 @@ __device__ __forceinline__ int swz_k(int row) {
 //   and frees stage it for the loads issued in the next slab;
 //   k-step KS-1: its fragments are already in registers, so its MFMAs start right after the
 //                barrier while step 0 of slab it+1 is read.
+// 256x256 tiles (kFront) instead issue all loads of slab it+S in k-step KS-1, into the stage the
+// barrier has just released (slab it's): S slabs are then in flight between barriers, and each
+// load has S-1 whole slabs of MFMAs to land (4-5% faster on 64K-row projections).
 // Loads are issued unconditionally (slab indices past the end are clamped to the last slab and
 // land in a stage that is never read again), so the loop body is one straight-line block that the
 // scheduling-group hints interleave: one MFMA, then one LDS read or one global load, so neither
@@ -463,10 +466,16 @@ void gemm_pipe_kernel(GemmArgs a) {
   static_assert(S >= 2, "at least two stages");
   constexpr int SLAB = (BM + BN) * BKS;  // 16-bit elements per stage: A rows, then B rows
   static_assert(NW * kEpilogueStageBytes <= S * SLAB * 2, "the epilogue's staging fits the LDS");
+  // Load schedule: 256x256 tiles issue all loads of slab it+S right after the barrier that ends the
+  // reads of slab it's stage (kFront: a whole slab before the barrier that first waits on them);
+  // smaller tiles spread the loads of slab it+S-1 over the k-steps before the barrier.
+  constexpr bool kFront = BM * BN >= 256 * 256;
   constexpr int kKeep = NLD * (S - 2);  // loads of younger slabs that stay in flight at a slab's end
-  static_assert(kKeep < 64, "vmcnt range");
-  // s_waitcnt vmcnt(kKeep) lgkmcnt(0), expcnt left free (gfx9 field layout: vmcnt bits 3:0 and 15:14)
+  constexpr int kKeepFirst = kFront ? NLD * (S - 1) : kKeep;  // the same after the prologue
+  static_assert(kKeepFirst < 64, "vmcnt range");
+  // s_waitcnt vmcnt(n) lgkmcnt(0), expcnt left free (gfx9 field layout: vmcnt bits 3:0 and 15:14)
   constexpr int kWaitSlab = (kKeep & 15) | ((kKeep >> 4) << 14) | (7 << 4);
+  constexpr int kWaitFirst = (kKeepFirst & 15) | ((kKeepFirst >> 4) << 14) | (7 << 4);
   constexpr int kWaitAll = 7 << 4;
   typedef typename Vec8<T>::type T8;
   typedef __attribute__((address_space(3))) void* LdsPtr;
@@ -580,23 +589,25 @@ void gemm_pipe_kernel(GemmArgs a) {
 
   if (n > 0) {
 #pragma unroll
-    for (int p = 0; p < S - 1; ++p)
+    for (int p = 0; p < (kFront ? S : S - 1); ++p)
 #pragma unroll
       for (int q = 0; q < NLD; ++q) issue(q, kb + min(p, n - 1), p);
-    __builtin_amdgcn_s_waitcnt(kWaitSlab);
+    __builtin_amdgcn_s_waitcnt(kWaitFirst);
     __builtin_amdgcn_s_barrier();
     fetch(0, 0, 0);
-    int cur = 0, ldst = S - 1;  // stage of slab it, stage receiving slab it+S-1
+    int cur = 0, ldst = S - 1;  // stage of slab it, stage receiving slab it+S-1 (spread schedule)
     for (int it = 0; it < n; ++it) {
-      const int lslab = kb + min(it + S - 1, n - 1);
+      const int lslab = kb + min(it + (kFront ? S : S - 1), n - 1);
       const int nxt = cur + 1 == S ? 0 : cur + 1;
 #pragma unroll
       for (int kk = 0; kk < KPRE; ++kk) {
+        if constexpr (!kFront) {
 #pragma unroll
-        for (int q = kk * LPS; q < (kk + 1) * LPS && q < NLD; ++q) issue(q, lslab, ldst);
+          for (int q = kk * LPS; q < (kk + 1) * LPS && q < NLD; ++q) issue(q, lslab, ldst);
+        }
         fetch(cur, kk + 1, (kk + 1) & 1);
         mma(kk & 1);
-        constexpr int nvm_max = LPS < NMF ? LPS : NMF;  // loads beyond the MFMA slots go unhinted
+        constexpr int nvm_max = kFront ? 0 : LPS < NMF ? LPS : NMF;  // loads beyond the MFMA slots go unhinted
         interleave(std::integral_constant<int, nvm_max>());
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -604,6 +615,11 @@ void gemm_pipe_kernel(GemmArgs a) {
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
       fetch(nxt, 0, 0);
+      if constexpr (kFront) {
+        // Every wave is past its reads of stage cur (this k-step runs from registers).
+#pragma unroll
+        for (int q = 0; q < NLD; ++q) issue(q, lslab, cur);
+      }
       mma((KS - 1) & 1);
       interleave(std::integral_constant<int, 0>());
       __builtin_amdgcn_sched_barrier(0);
