@@ -451,7 +451,7 @@ __device__ __forceinline__ int swz_k(int row) {
 // wave tiles whose accumulators alone take 256 registers: 8-wave workgroups own a CU, 4-wave ones
 // with smaller wave tiles share it with a second workgroup (whose main loop then covers this one's
 // epilogue).
-template <typename T, int BM, int BN, int WM, int WN, int BKS, int S, Epi E>
+template <typename T, int BM, int BN, int WM, int WN, int BKS, int S, Epi E, bool RING>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(BM * BN / (WM * WN) >= 128 * 128 ? 1 : 2)))
 void gemm_pipe_kernel(GemmArgs a) {
   constexpr int NW = WM * WN;
@@ -469,9 +469,13 @@ void gemm_pipe_kernel(GemmArgs a) {
   // Load schedule: 256x256 tiles issue all loads of slab it+S right after the barrier that ends the
   // reads of slab it's stage (kFront: a whole slab before the barrier that first waits on them);
   // smaller tiles spread the loads of slab it+S-1 over the k-steps before the barrier.
-  constexpr bool kFront = BM * BN >= 256 * 256;
-  constexpr int kKeep = NLD * (S - 2);  // loads of younger slabs that stay in flight at a slab's end
-  constexpr int kKeepFirst = kFront ? NLD * (S - 1) : kKeep;  // the same after the prologue
+  constexpr bool kFront = !RING && BM * BN >= 256 * 256;
+  // RING: the LDS holds five half-slab buffers (one operand's rows of one slab each), see below.
+  static_assert(!RING || (BM == BN && S == 5), "ring: five equal half-slab buffers");
+  constexpr int HALFE = BM * BKS;  // 16-bit elements of a ring buffer
+  // Loads of younger slabs (ring: of the youngest A half) that stay in flight at a slab's end.
+  constexpr int kKeep = RING ? AG : NLD * (S - 2);
+  constexpr int kKeepFirst = RING ? 2 * AG + BG : kFront ? NLD * (S - 1) : kKeep;  // after the prologue
   static_assert(kKeepFirst < 64, "vmcnt range");
   // s_waitcnt vmcnt(n) lgkmcnt(0), expcnt left free (gfx9 field layout: vmcnt bits 3:0 and 15:14)
   constexpr int kWaitSlab = (kKeep & 15) | ((kKeep >> 4) << 14) | (7 << 4);
@@ -526,11 +530,14 @@ void gemm_pipe_kernel(GemmArgs a) {
   // instruction (bound through the {m0} operand constraint, so the compiler writes it and knows it
   // is live; one s_nop between that write and the LDS DMA that reads it).
   const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>((LdsPtr)smem_raw));
-  auto issue = [&](int q, int kt, int st) {
+  auto issue_at = [&](int q, int kt, int base) {  // base: element offset of the load's LDS destination
     const T* g = src[q] + static_cast<size_t>(kt) * BKS;
-    const unsigned m0 = lds_base + static_cast<unsigned>(st * SLAB + dst[q]) * 2;
+    const unsigned m0 = lds_base + static_cast<unsigned>(base + dst[q]) * 2;
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0));
   };
+  auto issue = [&](int q, int kt, int st) { issue_at(q, kt, st * SLAB); };
+  // Ring buffers take one operand's rows: B loads drop the A rows' offset that dst[] carries.
+  auto issue_ring = [&](int q, int kt, int buf) { issue_at(q, kt, buf * HALFE - (q < AG ? 0 : BM * BKS)); };
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -542,9 +549,7 @@ void gemm_pipe_kernel(GemmArgs a) {
 
   const int lrow = lane & 31, kg = lane >> 5;
   T8 af[2][TM], bfr[2][TN];
-  auto fetch = [&](int st, int kk, int s) {
-    const T* cA = lds + st * SLAB;
-    const T* cB = cA + BM * BKS;
+  auto fetch_at = [&](const T* cA, const T* cB, int kk, int s) {
     const int ch = kk * 2 + kg;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -557,6 +562,7 @@ void gemm_pipe_kernel(GemmArgs a) {
       bfr[s][j] = *reinterpret_cast<const T8*>(cB + r * BKS + ((ch ^ swz_k<BKS>(r)) << 3));
     }
   };
+  auto fetch = [&](int st, int kk, int s) { fetch_at(lds + st * SLAB, lds + st * SLAB + BM * BKS, kk, s); };
   // Weights as the MFMA A operand: the accumulator holds C^T, so each lane ends with four
   // consecutive output columns of one row.
   auto mma = [&](int s) {
@@ -587,7 +593,49 @@ void gemm_pipe_kernel(GemmArgs a) {
   constexpr int KPRE = KS - 1;
   constexpr int LPS = (NLD + KPRE - 1) / KPRE;  // loads per pre-barrier k-step
 
-  if (n > 0) {
+  if (RING && n > 0) {
+    // Ring of five half-slab buffers (160 KB for 256x256 tiles): half h (slab h / 2, A rows for
+    // even h, B rows for odd) lives in buffer h % 5.  While slab it is consumed from halves 2it and
+    // 2it+1, halves 2it+2 .. 2it+4 are landed or in flight; the barrier after its last LDS reads
+    // waits for slab it+1 only, so the A half of slab it+2 stays in flight across it and the
+    // operand stream never drains; right after it, the two freed buffers take halves 2it+5 and
+    // 2it+6 (B of slab it+2, A of slab it+3).
+#pragma unroll
+    for (int h = 0; h < 5; ++h) {
+      const int kt = kb + min(h / 2, n - 1);
+#pragma unroll
+      for (int q = (h & 1) ? AG : 0; q < ((h & 1) ? NLD : AG); ++q) issue_ring(q, kt, h);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitFirst);
+    __builtin_amdgcn_s_barrier();
+    fetch_at(lds, lds + HALFE, 0, 0);
+    int abuf = 0;  // buffer of slab it's A half; its B half is in the next one
+    for (int it = 0; it < n; ++it) {
+      const int bbuf = abuf == 4 ? 0 : abuf + 1;
+      const int nabuf = abuf >= 3 ? abuf - 3 : abuf + 2, nbbuf = nabuf == 4 ? 0 : nabuf + 1;
+#pragma unroll
+      for (int kk = 0; kk < KPRE; ++kk) {
+        fetch_at(lds + abuf * HALFE, lds + bbuf * HALFE, kk + 1, (kk + 1) & 1);
+        mma(kk & 1);
+        interleave(std::integral_constant<int, 0>());
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitSlab);
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      fetch_at(lds + nabuf * HALFE, lds + nbbuf * HALFE, 0, 0);
+      const int kt2 = kb + min(it + 2, n - 1), kt3 = kb + min(it + 3, n - 1);
+#pragma unroll
+      for (int q = AG; q < NLD; ++q) issue_ring(q, kt2, abuf);
+#pragma unroll
+      for (int q = 0; q < AG; ++q) issue_ring(q, kt3, bbuf);
+      mma((KS - 1) & 1);
+      interleave(std::integral_constant<int, 0>());
+      __builtin_amdgcn_sched_barrier(0);
+      abuf = nabuf;
+    }
+  }
+  if (!RING && n > 0) {
 #pragma unroll
     for (int p = 0; p < (kFront ? S : S - 1); ++p)
 #pragma unroll
@@ -638,7 +686,8 @@ void gemm_pipe_kernel(GemmArgs a) {
 struct TileDef {
   int bm, bn, wm, wn;
   int pf;      // >= 2: register-staged kernel with pf slabs in flight; 0: pipelined direct-to-LDS kernel
-  int bk, st;  // pipelined kernel: slab depth and LDS stages
+  int bk, st;  // pipelined kernel: slab depth and LDS stages (ring: five half-slab buffers)
+  bool ring;
   int threads() const { return 64 * wm * wn; }
 };
 // Tile menu; the planner picks per problem.  Ids are part of the op-level ABI (tests sweep them).
@@ -666,11 +715,17 @@ constexpr TileDef kTiles[] = {
     {64, 128, 2, 2, 0, 64, 6},   // 16: wave 32x64
     {32, 128, 1, 4, 0, 64, 8},   // 17: wave 32x32, very small M
     {128, 128, 2, 2, 0, 64, 4},  // 18: wave 64x64
+    // 256x256 tiles whose operand stream stays in flight across the slab barriers (ring of five
+    // half-slab LDS buffers, 160 KB).
+    {256, 256, 2, 4, 0, 64, 5, true},  // 19: 8 waves of 128x64
+    {256, 256, 2, 2, 0, 64, 5, true},  // 20: 4 waves of 128x128
 };
 constexpr int kTileCount = sizeof(kTiles) / sizeof(kTiles[0]);
 
 constexpr size_t lds_bytes(const TileDef& d) {
-  return d.pf ? static_cast<size_t>(2) * (d.bm + d.bn) * BK * 2 : static_cast<size_t>(d.st) * (d.bm + d.bn) * d.bk * 2;
+  return d.pf     ? static_cast<size_t>(2) * (d.bm + d.bn) * BK * 2
+         : d.ring ? static_cast<size_t>(5) * d.bm * d.bk * 2
+                  : static_cast<size_t>(d.st) * (d.bm + d.bn) * d.bk * 2;
 }
 
 template <typename T, Epi E>
@@ -682,7 +737,9 @@ hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
 #define LAYA_TILE(ID, BM_, BN_, WM_, WN_, PF_) \
   case ID: hipLaunchKernelGGL((gemm_kernel<T, BM_, BN_, WM_, WN_, PF_, E>), grid, block, lds, stream, a); break;
 #define LAYA_PIPE(ID, BM_, BN_, WM_, WN_, BK_, ST_) \
-  case ID: hipLaunchKernelGGL((gemm_pipe_kernel<T, BM_, BN_, WM_, WN_, BK_, ST_, E>), grid, block, lds, stream, a); break;
+  case ID: hipLaunchKernelGGL((gemm_pipe_kernel<T, BM_, BN_, WM_, WN_, BK_, ST_, E, false>), grid, block, lds, stream, a); break;
+#define LAYA_RING(ID, BM_, BN_, WM_, WN_) \
+  case ID: hipLaunchKernelGGL((gemm_pipe_kernel<T, BM_, BN_, WM_, WN_, 64, 5, E, true>), grid, block, lds, stream, a); break;
     LAYA_PIPE(0, 256, 256, 2, 2, 64, 2)
     LAYA_PIPE(1, 256, 128, 2, 2, 64, 2)
     LAYA_TILE(2, 128, 128, 2, 2, 2)
@@ -702,6 +759,9 @@ hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
     LAYA_PIPE(16, 64, 128, 2, 2, 64, 6)
     LAYA_PIPE(17, 32, 128, 1, 4, 64, 8)
     LAYA_PIPE(18, 128, 128, 2, 2, 64, 4)
+    LAYA_RING(19, 256, 256, 2, 4)
+    LAYA_RING(20, 256, 256, 2, 2)
+#undef LAYA_RING
 #undef LAYA_TILE
 #undef LAYA_PIPE
     default: return hipErrorInvalidValue;
@@ -716,20 +776,22 @@ hipError_t set_lds_attr() {
   if (e == hipSuccess)                                                                                \
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(&__VA_ARGS__),                                \
                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds_bytes(kTiles[ID])));
-  LAYA_ATTR(0, gemm_pipe_kernel<T, 256, 256, 2, 2, 64, 2, E>)
-  LAYA_ATTR(1, gemm_pipe_kernel<T, 256, 128, 2, 2, 64, 2, E>)
+  LAYA_ATTR(0, gemm_pipe_kernel<T, 256, 256, 2, 2, 64, 2, E, false>)
+  LAYA_ATTR(1, gemm_pipe_kernel<T, 256, 128, 2, 2, 64, 2, E, false>)
   LAYA_ATTR(2, gemm_kernel<T, 128, 128, 2, 2, 2, E>)
-  LAYA_ATTR(7, gemm_pipe_kernel<T, 256, 256, 2, 4, 64, 2, E>)
-  LAYA_ATTR(8, gemm_pipe_kernel<T, 256, 128, 4, 2, 64, 2, E>)
-  LAYA_ATTR(9, gemm_pipe_kernel<T, 128, 256, 2, 4, 64, 2, E>)
-  LAYA_ATTR(11, gemm_pipe_kernel<T, 256, 256, 2, 4, 32, 4, E>)
-  LAYA_ATTR(12, gemm_pipe_kernel<T, 256, 128, 2, 2, 32, 3, E>)
-  LAYA_ATTR(13, gemm_pipe_kernel<T, 128, 256, 2, 2, 32, 3, E>)
-  LAYA_ATTR(14, gemm_pipe_kernel<T, 64, 64, 2, 2, 64, 8, E>)
-  LAYA_ATTR(15, gemm_pipe_kernel<T, 128, 64, 2, 2, 64, 6, E>)
-  LAYA_ATTR(16, gemm_pipe_kernel<T, 64, 128, 2, 2, 64, 6, E>)
-  LAYA_ATTR(17, gemm_pipe_kernel<T, 32, 128, 1, 4, 64, 8, E>)
-  LAYA_ATTR(18, gemm_pipe_kernel<T, 128, 128, 2, 2, 64, 4, E>)
+  LAYA_ATTR(7, gemm_pipe_kernel<T, 256, 256, 2, 4, 64, 2, E, false>)
+  LAYA_ATTR(8, gemm_pipe_kernel<T, 256, 128, 4, 2, 64, 2, E, false>)
+  LAYA_ATTR(9, gemm_pipe_kernel<T, 128, 256, 2, 4, 64, 2, E, false>)
+  LAYA_ATTR(11, gemm_pipe_kernel<T, 256, 256, 2, 4, 32, 4, E, false>)
+  LAYA_ATTR(12, gemm_pipe_kernel<T, 256, 128, 2, 2, 32, 3, E, false>)
+  LAYA_ATTR(13, gemm_pipe_kernel<T, 128, 256, 2, 2, 32, 3, E, false>)
+  LAYA_ATTR(14, gemm_pipe_kernel<T, 64, 64, 2, 2, 64, 8, E, false>)
+  LAYA_ATTR(15, gemm_pipe_kernel<T, 128, 64, 2, 2, 64, 6, E, false>)
+  LAYA_ATTR(16, gemm_pipe_kernel<T, 64, 128, 2, 2, 64, 6, E, false>)
+  LAYA_ATTR(17, gemm_pipe_kernel<T, 32, 128, 1, 4, 64, 8, E, false>)
+  LAYA_ATTR(18, gemm_pipe_kernel<T, 128, 128, 2, 2, 64, 4, E, false>)
+  LAYA_ATTR(19, gemm_pipe_kernel<T, 256, 256, 2, 4, 64, 5, E, true>)
+  LAYA_ATTR(20, gemm_pipe_kernel<T, 256, 256, 2, 2, 64, 5, E, true>)
 #undef LAYA_ATTR
   return e;
 }
@@ -780,11 +842,13 @@ void gemm_plan(int M, int N, int K, Epi epi, DType t, int cus, int* tile, int* s
   // Largest tile that still gives every CU a workgroup; small problems fall back to small tiles
   // and, for the fp32 (split-K capable) epilogue, to K splits until the grid covers the chip.
   // Eight-wave tiles first: with two waves per SIMD they sustain the most MFMA throughput when
-  // the grid is large enough; then the pipelined four-wave tiles from large to small (measured
-  // 13-21% faster than the register-staged tiles of the same shapes on 512-row problems).
+  // the grid is large enough (the 256x256 one as the ring, whose operand stream stays in flight
+  // across slab barriers: up to 7% faster than tile 7 on 64K-row projections); then the pipelined
+  // four-wave tiles from large to small (measured 13-21% faster than the register-staged tiles of
+  // the same shapes on 512-row problems).
   // Tile 10 is only the RoPE fallback for N not a multiple of 128 (odd head counts): every other
   // RoPE-capable tile is 128 or more columns wide.
-  const int order[] = {7, 9, 8, 0, 1, 18, 15, 16, 14, 17};
+  const int order[] = {19, 9, 8, 20, 1, 18, 15, 16, 14, 17};
   int best = rope ? (N % 128 ? 10 : 16) : 14, best_split = 1;
   for (int id : order) {
     const TileDef& d = kTiles[id];

@@ -164,7 +164,7 @@ def linear(x, w, bias, out, kind, dtype, M, N, K, splits, tile):
     sync()
 
 
-GEMM_TILES = 19  # tile ids of laya_op_linear (csrc/gemm.hip kTiles)
+GEMM_TILES = 21  # tile ids of laya_op_linear (csrc/gemm.hip kTiles)
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
@@ -181,7 +181,7 @@ def test_linear_tiles_match_fp32_product(gpu, dtype, tile):
                                    atol=1e-4, rtol=1e-4)
 
 
-@pytest.mark.parametrize("tile", [5, 11, 12, 14, 17])
+@pytest.mark.parametrize("tile", [5, 11, 12, 14, 17, 19])
 @pytest.mark.parametrize("splits", [2, 3, 4])
 def test_linear_split_k_partials_sum_to_the_product(gpu, splits, tile):
     t = torch()
@@ -225,7 +225,7 @@ def test_linear_gelu_epilogue(gpu, dtype):
     np.testing.assert_allclose(from16(out), expected, atol=tol, rtol=tol)
 
 
-@pytest.mark.parametrize("tile", [0, 2, 5, 6, 7, 9, 11, 12, 13, 14, 16, 18])
+@pytest.mark.parametrize("tile", [0, 2, 5, 6, 7, 9, 11, 12, 13, 14, 16, 18, 19, 20])
 def test_qkv_epilogue_writes_head_major_layout(gpu, tile):
     """Integer-valued operands make the product exact, so the layout check is bit-exact."""
     t = torch()
