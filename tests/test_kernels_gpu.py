@@ -181,6 +181,25 @@ def test_linear_tiles_match_fp32_product(gpu, dtype, tile):
                                    atol=1e-4, rtol=1e-4)
 
 
+@pytest.mark.parametrize("kind", [1, 2])
+@pytest.mark.parametrize("tile", range(GEMM_TILES))
+def test_linear_16bit_epilogues_every_tile(gpu, tile, kind):
+    """Bias, optional GELU and the single rounding through each tile's staged row stores, with
+    rows past a tile boundary."""
+    t = torch()
+    rng = np.random.default_rng(100 + tile)
+    M, N, K = 300, 512, 256
+    x = half_round(rng.normal(0, 1, (M, K)), "f16")
+    w = half_round(rng.normal(0, 1 / math.sqrt(K), (N, K)), "f16")
+    bias = rng.normal(0, .5, N).astype(np.float32)
+    out = t.full((M, N), float("nan"), dtype=t.float16, device=gpu)
+    linear(to16(x, "f16", gpu), to16(w, "f16", gpu), dev(bias, gpu), out, kind, "f16", M, N, K, 1, tile)
+    expected = (x.astype(np.float64) @ w.T.astype(np.float64) + bias).astype(np.float32)
+    if kind == 2:
+        expected = E.gelu(expected)
+    np.testing.assert_allclose(from16(out), expected, atol=2e-3, rtol=2e-3)
+
+
 @pytest.mark.parametrize("tile", [5, 11, 12, 14, 17, 19])
 @pytest.mark.parametrize("splits", [2, 3, 4])
 def test_linear_split_k_partials_sum_to_the_product(gpu, splits, tile):
