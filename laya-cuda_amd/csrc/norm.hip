@@ -41,7 +41,13 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(EmbedArgs a) {
   if (a.out16) store_row16<D, T>(static_cast<T*>(a.out16) + static_cast<size_t>(row) * D, lane, v);
 }
 
-template <int D, typename T>
+// NS: the number of split-K partials when it is known at launch (1..kMaxFixedSplits), so that
+// every partial's row, the bias and the residual are loaded before the first add (one memory round
+// trip; a loop over a run-time split count waited for each partial in turn); 0: no partials (the
+// 16-bit branch, or none); -1: any other split count, loaded in a loop.
+constexpr int kMaxFixedSplits = 8;
+
+template <int D, typename T, int NS>
 __global__ __launch_bounds__(256) void add_norm_kernel(AddNormArgs a) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -51,9 +57,24 @@ __global__ __launch_bounds__(256) void add_norm_kernel(AddNormArgs a) {
   if (a.gamma) np.load(a.gamma, a.beta, lane);
   float v[D / 64];
   load_row<D>(a.residual + off, lane, v);
-  if (a.parts) {
+  if constexpr (NS > 0) {
     // branch = sum of the split-K partial products, then + bias, then added to the residual:
     // one fp32 rounding per add, in a fixed order, so graph replays are bit-identical.
+    float br[NS][D / 64], bias[D / 64];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) load_row<D>(a.parts + static_cast<size_t>(s) * a.part_stride + off, lane, br[s]);
+    if (a.bias) load_row<D>(a.bias, lane, bias);
+#pragma unroll
+    for (int s = 1; s < NS; ++s)
+#pragma unroll
+      for (int i = 0; i < D / 64; ++i) br[0][i] = br[0][i] + br[s][i];
+    if (a.bias) {
+#pragma unroll
+      for (int i = 0; i < D / 64; ++i) br[0][i] = br[0][i] + bias[i];
+    }
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) v[i] = v[i] + br[0][i];
+  } else if constexpr (NS < 0) {
     float br[D / 64];
     load_row<D>(a.parts + off, lane, br);
     for (int s = 1; s < a.splits; ++s) {
@@ -103,11 +124,22 @@ hipError_t launch_embed_t(const EmbedArgs& a, int width, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <typename T, int D>
+void launch_add_norm_d(const AddNormArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
+  const int ns = !a.parts ? 0 : a.splits <= kMaxFixedSplits ? a.splits : -1;
+  switch (ns) {
+#define LAYA_NS(N) case N: hipLaunchKernelGGL((add_norm_kernel<D, T, N>), grid, block, 0, stream, a); break;
+    LAYA_NS(0) LAYA_NS(1) LAYA_NS(2) LAYA_NS(3) LAYA_NS(4) LAYA_NS(5) LAYA_NS(6) LAYA_NS(7) LAYA_NS(8)
+#undef LAYA_NS
+    default: hipLaunchKernelGGL((add_norm_kernel<D, T, -1>), grid, block, 0, stream, a); break;
+  }
+}
+
 template <typename T>
 hipError_t launch_add_norm_t(const AddNormArgs& a, int width, hipStream_t stream) {
   const dim3 grid((a.rows + 3) / 4), block(256);
   switch (width) {
-#define LAYA_CASE(D) case D: hipLaunchKernelGGL((add_norm_kernel<D, T>), grid, block, 0, stream, a); break;
+#define LAYA_CASE(D) case D: launch_add_norm_d<T, D>(a, grid, block, stream); break;
     LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
     LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
 #undef LAYA_CASE
