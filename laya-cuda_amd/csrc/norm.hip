@@ -46,11 +46,12 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(EmbedArgs a) {
 // trip; a loop over a run-time split count waited for each partial in turn); 0: no partials (the
 // 16-bit branch, or none); -1: any other split count, loaded in a loop.
 constexpr int kMaxFixedSplits = 8;
+constexpr int kOneWaveRows = 4096;
 
 template <int D, typename T, int NS>
 __global__ __launch_bounds__(256) void add_norm_kernel(AddNormArgs a) {
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= a.rows) return;
   const size_t off = static_cast<size_t>(row) * D;
   NormParams<D> np;
@@ -137,7 +138,11 @@ void launch_add_norm_d(const AddNormArgs& a, dim3 grid, dim3 block, hipStream_t 
 
 template <typename T>
 hipError_t launch_add_norm_t(const AddNormArgs& a, int width, hipStream_t stream) {
-  const dim3 grid((a.rows + 3) / 4), block(256);
+  // A wave per row.  Few rows (batch-1 requests): one-wave workgroups, so the rows spread over
+  // every CU and each CU fetches fewer of them (the fill of one CU, not HBM, bounds these
+  // launches); many rows: four-wave workgroups.
+  const int wpb = a.rows <= kOneWaveRows ? 1 : 4;
+  const dim3 grid((a.rows + wpb - 1) / wpb), block(64 * wpb);
   switch (width) {
 #define LAYA_CASE(D) case D: launch_add_norm_d<T, D>(a, grid, block, stream); break;
     LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
