@@ -112,16 +112,23 @@ __global__ __launch_bounds__(256) void head_logit_kernel(HeadLogitArgs a) {
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= a.cap || r >= *a.n_sel) return;
   const size_t off = static_cast<size_t>(r) * D;
-  float v[D / 64], t[D / 64];
-  load_row<D>(a.parts + off, lane, v);
-  for (int s = 1; s < a.splits; ++s) {
-    load_row<D>(a.parts + s * a.split_stride + off, lane, t);
-#pragma unroll
-    for (int i = 0; i < D / 64; ++i) v[i] = v[i] + t[i];
-  }
   float b1[D / 64], w3[D / 64];
   load_row<D>(a.b1, lane, b1);
   load_row<D>(a.w3, lane, w3);
+  // Partials summed in split order; loaded four at a time (clamped to the last split, whose copies
+  // are not added) so each group costs one memory round trip instead of one per split.
+  float v[D / 64];
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) v[i] = 0.f;
+  for (int s0 = 0; s0 < a.splits; s0 += 4) {
+    float t[4][D / 64];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load_row<D>(a.parts + min(s0 + u, a.splits - 1) * a.split_stride + off, lane, t[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int i = 0; i < D / 64; ++i) v[i] = s0 + u < a.splits ? v[i] + t[u][i] : v[i];
+  }
   float dot = 0.f;
 #pragma unroll
   for (int i = 0; i < D / 64; ++i) dot += gelu(v[i] + b1[i]) * w3[i];
@@ -194,9 +201,17 @@ __global__ __launch_bounds__(256) void act_out_kernel(ActOutArgs a) {
   extern __shared__ float hid[];  // [hidden]
   for (int o = tid; o < a.hidden; o += 256) {
     const size_t off = static_cast<size_t>(q) * a.hidden + o;
-    float v = a.parts[off];
-    for (int s = 1; s < a.splits; ++s) v = v + a.parts[s * a.split_stride + off];
-    hid[o] = gelu(v + a.a0b[o]);
+    // Partials summed in split order, loaded eight at a time (one round trip per group).
+    const float bias = a.a0b[o];
+    float v = 0.f;
+    for (int s0 = 0; s0 < a.splits; s0 += 8) {
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = a.parts[min(s0 + u, a.splits - 1) * a.split_stride + off];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v = s0 + u < a.splits ? v + t[u] : v;
+    }
+    hid[o] = gelu(v + bias);
   }
   __syncthreads();
   for (int o = wave; o < a.n_act; o += 4) {
