@@ -62,31 +62,51 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherRowsArgs a) {
 }
 
 // fp32 GEMM on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): parts[z] = X W^T over split z.
-// Workgroup tile 32 rows x 64 cols, 4 waves of 16x32; K staged in 32-wide LDS slabs.
+// Workgroup tile 32 rows x 64 cols, 4 waves of 16x32.  The split's K range is staged in LDS up to
+// 128 columns at a time, every 16-byte load of a chunk issued before the first LDS store, so a
+// split of up to 128 columns costs one memory round trip (these tiny products are all latency).
 __global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
-  constexpr int BM = 32, BN = 64, BKH = 32;
+  constexpr int BM = 32, BN = 64, KC = 128, KP = KC + 4;  // pitch KP: 16-byte rows, conflict-free reads
+  constexpr int AV = BM * KC / 4 / 256, BV = BN * KC / 4 / 256;  // float4 loads per thread per chunk
   const int rows = min(a.cap, *a.n_rows);
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, z = blockIdx.z;
   if (m0 >= rows) return;
-  __shared__ float sA[BM][BKH + 1];
-  __shared__ float sB[BN][BKH + 1];
+  __shared__ __align__(16) float sA[BM][KP];
+  __shared__ __align__(16) float sB[BN][KP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = (wave >> 1) * 16, wn = (wave & 1) * 32;
-  const int per = a.K / a.splits;
+  const int per = a.K / a.splits;  // a multiple of 32
   const int kb = z * per, ke = kb + per;
   f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  for (int k0 = kb; k0 < ke; k0 += BKH) {
-    for (int e = tid; e < BM * BKH; e += 256) {
-      const int r = e / BKH, c = e % BKH;
-      sA[r][c] = m0 + r < rows ? a.x[static_cast<size_t>(m0 + r) * a.K + k0 + c] : 0.f;
+  for (int k0 = kb; k0 < ke; k0 += KC) {
+    const int kn = min(KC, ke - k0);
+    // Chunk loads, all in flight together: rows past `rows` and columns past the split read a
+    // clamped in-range address and are zeroed (A) or never multiplied (columns >= kn).
+    f32x4 ra[AV], rb[BV];
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+      const int e = tid + 256 * i, r = e / (KC / 4), c = 4 * (e % (KC / 4));
+      const int rr = min(m0 + r, rows - 1), cc = min(c, kn - 4);
+      ra[i] = *reinterpret_cast<const f32x4*>(a.x + static_cast<size_t>(rr) * a.K + k0 + cc);
+      if (m0 + r >= rows) ra[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    for (int e = tid; e < BN * BKH; e += 256) {
-      const int r = e / BKH, c = e % BKH;
-      sB[r][c] = a.w[static_cast<size_t>(n0 + r) * a.K + k0 + c];
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+      const int e = tid + 256 * i, r = e / (KC / 4), c = 4 * (e % (KC / 4));
+      rb[i] = *reinterpret_cast<const f32x4*>(a.w + static_cast<size_t>(n0 + r) * a.K + k0 + min(c, kn - 4));
+    }
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+      const int e = tid + 256 * i, r = e / (KC / 4), c = 4 * (e % (KC / 4));
+      *reinterpret_cast<f32x4*>(&sA[r][c]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+      const int e = tid + 256 * i, r = e / (KC / 4), c = 4 * (e % (KC / 4));
+      *reinterpret_cast<f32x4*>(&sB[r][c]) = rb[i];
     }
     __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < BKH; kk += 4) {
+    for (int kk = 0; kk < kn; kk += 4) {
       const float av = sA[wm + (lane & 15)][kk + (lane >> 4)];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
