@@ -79,7 +79,8 @@ constexpr int kEpilogueStageBytes = 32 * 36 * 4;
 // done with LDS: its last barrier has passed).
 template <typename T, int BM, int BN, int WM, int WN, Epi E, bool kEarlyBias>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
-                                              const float4 (&early_bias)[4], int m0, int n0, int z,
+                                              const float4 (&early_bias)[kEarlyBias ? BN / WN / 32 : 1][4],
+                                              int m0, int n0, int z,
                                               unsigned char* smem_raw, int lane, int wave) {
   constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
@@ -94,7 +95,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[B
     v[2] = acc[i][j][4 * r4 + 2];
     v[3] = acc[i][j][4 * r4 + 3];
     if (with_bias) {
-      const float4 b = kEarlyBias ? early_bias[r4]
+      const float4 b = kEarlyBias ? early_bias[kEarlyBias ? j : 0][r4]
                                   : *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + j * 32 + 8 * r4 + 4 * kg);
       v[0] = v[0] + b.x; v[1] = v[1] + b.y; v[2] = v[2] + b.z; v[3] = v[3] + b.w;
     }
@@ -334,11 +335,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
   // latency hides under the main loop instead of opening the epilogue.
   constexpr bool kEarlyBias = TN == 1;
   const bool with_bias = (E != Epi::F32 || a.splits == 1) && a.bias;
-  float4 early_bias[4];
+  float4 early_bias[1][4];
   if constexpr (kEarlyBias) {
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4)
-      early_bias[r4] = with_bias ? *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + 8 * r4 + 4 * kg)
+      early_bias[0][r4] = with_bias ? *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + 8 * r4 + 4 * kg)
                                  : make_float4(0.f, 0.f, 0.f, 0.f);
   }
   // One 64-deep slab from LDS buffer `buf`: four 16-deep MFMA steps.  With at most 8 MFMA tiles per
@@ -522,6 +523,25 @@ void gemm_pipe_kernel(GemmArgs a) {
       }
     }
   }
+  // Small tiles (batch-1 problems) fetch their bias (16 floats per 32 columns per lane) before the
+  // main loop: loaded in the epilogue it cost one more memory round trip at the end of every launch.
+  // The load is older than every operand load, and loads complete in order, so the main loop's
+  // vmcnt waits cover it.
+  constexpr bool kEarlyBias = BM * BN <= 128 * 128 && TN <= 2;
+  float4 early_bias[kEarlyBias ? TN : 1][4];
+  if constexpr (kEarlyBias) {
+    const bool with_bias = (E != Epi::F32 || a.splits == 1) && a.bias;
+    const int kg = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        early_bias[j][r4] = with_bias ? *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + j * 32 + 8 * r4 + 4 * kg)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) early_bias[0][r4] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   // The loads are issued from inline assembly: the compiler's own global_load_lds makes its wait
   // counter model assume each one may overwrite any LDS a pending read targets, so it drains all LDS
   // reads before every load and serialises the fragment reads of the next k-step with the MFMAs.
@@ -679,8 +699,7 @@ void gemm_pipe_kernel(GemmArgs a) {
   // reuses LDS.
   __builtin_amdgcn_s_waitcnt(kWaitAll);
   __syncthreads();
-  const float4 no_bias[4] = {};
-  gemm_epilogue<T, BM, BN, WM, WN, E, false>(a, acc, no_bias, m0, n0, z, smem_raw, lane, wave);
+  gemm_epilogue<T, BM, BN, WM, WN, E, kEarlyBias>(a, acc, early_bias, m0, n0, z, smem_raw, lane, wave);
 }
 
 struct TileDef {
