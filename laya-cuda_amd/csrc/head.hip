@@ -68,9 +68,11 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherRowsArgs a) {
 __global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
   constexpr int BM = 32, BN = 64, KC = 128, KP = KC + 4;  // pitch KP: 16-byte rows, conflict-free reads
   constexpr int AV = BM * KC / 4 / 256, BV = BN * KC / 4 / 256;  // float4 loads per thread per chunk
-  const int rows = min(a.cap, *a.n_rows);
+  // The live row count is a device scalar of this request; it is only consulted for the stores,
+  // so its load does not delay the operand loads (rows up to the capacity are in the buffers).
+  const int n_rows = *a.n_rows;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, z = blockIdx.z;
-  if (m0 >= rows) return;
+  if (m0 >= a.cap) return;
   __shared__ __align__(16) float sA[BM][KP];
   __shared__ __align__(16) float sB[BN][KP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -80,15 +82,14 @@ __global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
   f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
   for (int k0 = kb; k0 < ke; k0 += KC) {
     const int kn = min(KC, ke - k0);
-    // Chunk loads, all in flight together: rows past `rows` and columns past the split read a
-    // clamped in-range address and are zeroed (A) or never multiplied (columns >= kn).
+    // Chunk loads, all in flight together: rows past the capacity and columns past the split read
+    // a clamped in-range address; such rows are never stored, such columns never multiplied.
     f32x4 ra[AV], rb[BV];
 #pragma unroll
     for (int i = 0; i < AV; ++i) {
       const int e = tid + 256 * i, r = e / (KC / 4), c = 4 * (e % (KC / 4));
-      const int rr = min(m0 + r, rows - 1), cc = min(c, kn - 4);
+      const int rr = min(m0 + r, a.cap - 1), cc = min(c, kn - 4);
       ra[i] = *reinterpret_cast<const f32x4*>(a.x + static_cast<size_t>(rr) * a.K + k0 + cc);
-      if (m0 + r >= rows) ra[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int i = 0; i < BV; ++i) {
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int row = m0 + wm + 4 * (lane >> 4) + e, col = n0 + wn + t * 16 + (lane & 15);
-      if (row < rows) a.parts[z * a.split_stride + static_cast<size_t>(row) * a.N + col] = acc[t][e];
+      if (row < a.cap && row < n_rows) a.parts[z * a.split_stride + static_cast<size_t>(row) * a.N + col] = acc[t][e];
     }
 }
 
@@ -130,7 +131,8 @@ template <int D>
 __global__ __launch_bounds__(256) void head_logit_kernel(HeadLogitArgs a) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= a.cap || r >= *a.n_sel) return;
+  if (r >= a.cap) return;
+  const int n_sel = *a.n_sel;  // consulted only before the stores (rows up to the capacity exist)
   const size_t off = static_cast<size_t>(r) * D;
   float b1[D / 64], w3[D / 64];
   load_row<D>(a.b1, lane, b1);
@@ -153,6 +155,7 @@ __global__ __launch_bounds__(256) void head_logit_kernel(HeadLogitArgs a) {
 #pragma unroll
   for (int i = 0; i < D / 64; ++i) dot += gelu(v[i] + b1[i]) * w3[i];
   const float logit = wave_sum(dot) + a.b3[0];
+  if (r >= n_sel) return;
   if (lane == 0) {
     const int q = a.sel_q[r];
     a.row_logit[r] = logit;
@@ -216,7 +219,7 @@ __global__ __launch_bounds__(256) void head_features_kernel(HeadFeatureArgs a) {
 // one wave per act output.
 __global__ __launch_bounds__(256) void act_out_kernel(ActOutArgs a) {
   const int q = blockIdx.x;
-  if (q >= *a.n_q) return;
+  const int n_q = *a.n_q;  // consulted only before the stores (all b question slots exist)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   extern __shared__ float hid[];  // [hidden]
   for (int o = tid; o < a.hidden; o += 256) {
@@ -239,7 +242,7 @@ __global__ __launch_bounds__(256) void act_out_kernel(ActOutArgs a) {
     float s = 0.f;
     for (int e = lane; e < a.hidden; e += 64) s += hid[e] * w[e];
     s = wave_sum(s);
-    if (lane == 0) a.acts[static_cast<size_t>(q) * a.n_act + o] = s + a.a2b[o];
+    if (lane == 0 && q < n_q) a.acts[static_cast<size_t>(q) * a.n_act + o] = s + a.a2b[o];
   }
 }
 
