@@ -153,7 +153,7 @@ int laya_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_se
                          int32_t* tiles, int max_tiles);
 /* Query rows per tile of an attention kernel: mode 0 (K/V blocks staged once in LDS and shared by
  * `waves` = 1, 2, 4 or 8 waves of 32 queries each; large batches) -> 32*waves; mode 1 (one tile of
- * 32 queries whose keys are split across `waves` = 2 or 4 waves; batch-1 latency) -> 32.  -1
+ * 32 queries whose keys are split across `waves` = 2, 4 or 8 waves; batch-1 latency) -> 32.  -1
  * for an invalid pair. */
 int laya_attention_block(int mode, int waves);
 

@@ -440,6 +440,7 @@ hipError_t launch_t(const AttnArgs& a, int mode, int waves, hipStream_t stream) 
     switch (waves) {
       case 2: hipLaunchKernelGGL((attention_split_kernel<T, 2>), grid, dim3(128), 0, stream, a); break;
       case 4: hipLaunchKernelGGL((attention_split_kernel<T, 4>), grid, dim3(256), 0, stream, a); break;
+      case 8: hipLaunchKernelGGL((attention_split_kernel<T, 8>), grid, dim3(512), 0, stream, a); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -494,7 +495,7 @@ int build_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_s
 
 bool attention_mode_valid(int mode, int waves) {
   if (mode == kAttnSharedKV) return waves == 1 || waves == 2 || waves == 4 || waves == 8;
-  if (mode == kAttnSplitKeys) return waves == 2 || waves == 4;
+  if (mode == kAttnSplitKeys) return waves == 2 || waves == 4 || waves == 8;
   return false;
 }
 

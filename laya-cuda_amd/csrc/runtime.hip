@@ -378,13 +378,14 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
       s->attn_mode = kAttnSharedKV;
       s->attn_waves = 8;
     } else {
-      // Each 32-query tile's keys split across waves.  Four waves halve the serial key blocks per
-      // wave, but the kernel's registers (one wave per SIMD) leave room for one such workgroup per
-      // CU: measured 6.6 against 8.7 us at 512 tokens (192 workgroups, one round), while at 1,024
-      // tokens (384 workgroups) two waves, two workgroups per CU and one round win, 15.9 against
-      // 17.8 us.
+      // Each 32-query tile's keys split across waves.  More waves shorten the serial key blocks
+      // per wave while the workgroups fit one round on the CUs (one workgroup per CU: four waves
+      // hold one per SIMD, eight two); at 512 tokens four waves measured 6.6 against 8.7 us for two
+      // (192 workgroups), while at 1,024 tokens (384 workgroups) two waves, two workgroups per CU
+      // and one round win, 15.9 against 17.8 us.
       s->attn_mode = kAttnSplitKeys;
-      s->attn_waves = static_cast<long long>((m + 31) / 32) * c.heads <= E.cus ? 4 : 2;
+      const bool one_round = static_cast<long long>((m + 31) / 32) * c.heads <= E.cus;
+      s->attn_waves = !one_round ? 2 : m >= 8 * 64 ? 8 : 4;
     }
     // Tiles of at most `block` rows: every sequence, and every run of rows between or after
     // sequences, adds at most one partial tile, so this bounds the work list of any request.
@@ -1284,7 +1285,7 @@ int laya_op_attention(const void* q, const void* k, const void* vt, void* out, c
                       int heads, int max_tiles, int mode, int waves, int window, int dtype16, void* stream) {
   return guarded(nullptr, [&] {
     LAYA_REQUIRE(attention_mode_valid(mode, waves),
-                 "mode 0 (shared K/V) takes 1, 2, 4 or 8 waves; mode 1 (split keys) takes 2 or 4");
+                 "mode 0 (shared K/V) takes 1, 2, 4 or 8 waves; mode 1 (split keys) takes 2, 4 or 8");
     LAYA_REQUIRE(m % 16 == 0, "rows must be a multiple of 16");
     LAYA_REQUIRE((reinterpret_cast<uintptr_t>(tiles) & 15) == 0, "tile list must be 16-byte aligned");
     AttnArgs a{q, k, vt, out, tiles, m, heads, max_tiles, window < 0 ? -1 : window};
