@@ -381,8 +381,8 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
       // Each 32-query tile's keys split across waves.  More waves shorten the serial key blocks
       // per wave while the workgroups fit one round on the CUs (one workgroup per CU: four waves
       // hold one per SIMD, eight two); at 512 tokens four waves measured 6.6 against 8.7 us for two
-      // (192 workgroups), while at 1,024 tokens (384 workgroups) two waves, two workgroups per CU
-      // and one round win, 15.9 against 17.8 us.
+      // (192 workgroups) and eight waves, one 64-key block each, 6.1 us, while at 1,024 tokens
+      // (384 workgroups) two waves, two workgroups per CU and one round win, 15.9 against 17.8 us.
       s->attn_mode = kAttnSplitKeys;
       const bool one_round = static_cast<long long>((m + 31) / 32) * c.heads <= E.cus;
       s->attn_waves = !one_round ? 2 : m >= 8 * 64 ? 8 : 4;
