@@ -9,6 +9,7 @@ from pathlib import Path
 LIBRARY = Path(__file__).with_name("liblaya_hip.so")
 
 OK, EINVAL, EDEVICE, ENOMEM, ESTATE = range(5)
+ABI_VERSION = 1  # LAYA_ABI_VERSION of the struct layouts mirrored below
 F32, F16, BF16 = 0, 1, 2
 NORM_POST, NORM_PRE = 0, 1
 POS_LEARNED, POS_ROPE = 0, 1
@@ -74,6 +75,9 @@ def load():
         for name, (args, ret) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes, fn.restype = args, ret
+        if lib.laya_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIBRARY} has ABI version {lib.laya_abi_version()}, this binding "
+                               f"mirrors version {ABI_VERSION}; rebuild the library")
         _lib = lib
     return _lib
 
