@@ -31,6 +31,14 @@ def test_library_exports_every_declared_symbol():
     assert lib.laya_abi_version() == _lib.ABI_VERSION == 1
 
 
+def test_binding_refuses_a_library_of_another_abi_version(monkeypatch):
+    monkeypatch.setattr(_lib, "_lib", None)  # force a fresh load
+    monkeypatch.setattr(_lib, "ABI_VERSION", _lib.ABI_VERSION + 1)
+    with pytest.raises(RuntimeError, match="ABI version"):
+        _lib.load()
+    assert _lib._lib is None  # nothing half-loaded is cached
+
+
 def test_packed_block_size_matches_the_python_packer():
     from laya_cuda.runtime import pack
     lib = _lib.load()
