@@ -452,6 +452,17 @@ __device__ __forceinline__ int swz_k(int row) {
 // wave tiles whose accumulators alone take 256 registers: 8-wave workgroups own a CU, 4-wave ones
 // with smaller wave tiles share it with a second workgroup (whose main loop then covers this one's
 // epilogue).
+// Publishes LDS stages written by direct-to-LDS loads: wait for this wave's loads (and LDS reads)
+// up to `wait`, then one workgroup barrier.  s_waitcnt and s_barrier are intrinsics without memory
+// semantics in LLVM IR, so the empty asm with a memory clobber keeps the compiler from moving the
+// following LDS fragment reads above them; it emits no instruction.
+template <int kWait>
+__device__ __forceinline__ void publish_stage() {
+  __builtin_amdgcn_s_waitcnt(kWait);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <typename T, int BM, int BN, int WM, int WN, int BKS, int S, Epi E, bool RING>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(BM * BN / (WM * WN) >= 128 * 128 ? 1 : 2)))
 void gemm_pipe_kernel(GemmArgs a) {
@@ -626,8 +637,7 @@ void gemm_pipe_kernel(GemmArgs a) {
 #pragma unroll
       for (int q = (h & 1) ? AG : 0; q < ((h & 1) ? NLD : AG); ++q) issue_ring(q, kt, h);
     }
-    __builtin_amdgcn_s_waitcnt(kWaitFirst);
-    __builtin_amdgcn_s_barrier();
+    publish_stage<kWaitFirst>();
     fetch_at(lds, lds + HALFE, 0, 0);
     int abuf = 0;  // buffer of slab it's A half; its B half is in the next one
     for (int it = 0; it < n; ++it) {
@@ -640,8 +650,7 @@ void gemm_pipe_kernel(GemmArgs a) {
         interleave(std::integral_constant<int, 0>());
         __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_s_waitcnt(kWaitSlab);
-      __builtin_amdgcn_s_barrier();
+      publish_stage<kWaitSlab>();
       __builtin_amdgcn_sched_barrier(0);
       fetch_at(lds + nabuf * HALFE, lds + nbbuf * HALFE, 0, 0);
       const int kt2 = kb + min(it + 2, n - 1), kt3 = kb + min(it + 3, n - 1);
@@ -660,8 +669,7 @@ void gemm_pipe_kernel(GemmArgs a) {
     for (int p = 0; p < (kFront ? S : S - 1); ++p)
 #pragma unroll
       for (int q = 0; q < NLD; ++q) issue(q, kb + min(p, n - 1), p);
-    __builtin_amdgcn_s_waitcnt(kWaitFirst);
-    __builtin_amdgcn_s_barrier();
+    publish_stage<kWaitFirst>();
     fetch(0, 0, 0);
     int cur = 0, ldst = S - 1;  // stage of slab it, stage receiving slab it+S-1 (spread schedule)
     for (int it = 0; it < n; ++it) {
@@ -679,8 +687,7 @@ void gemm_pipe_kernel(GemmArgs a) {
         interleave(std::integral_constant<int, nvm_max>());
         __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_s_waitcnt(kWaitSlab);
-      __builtin_amdgcn_s_barrier();
+      publish_stage<kWaitSlab>();
       __builtin_amdgcn_sched_barrier(0);
       fetch(nxt, 0, 0);
       if constexpr (kFront) {

@@ -72,12 +72,17 @@ def load():
             raise RuntimeError(f"{LIBRARY} is missing; build it with `make -C laya-cuda_amd/csrc` "
                                "(or __graft_entry__.build()).  There is no CPU fallback.")
         lib = ct.CDLL(str(LIBRARY))
+        # The version first: a library of another ABI may lack or rename the other exports.
+        version = getattr(lib, "laya_abi_version", None)
+        if version is None:
+            raise RuntimeError(f"{LIBRARY} exports no laya_abi_version; rebuild the library")
+        version.argtypes, version.restype = [], ct.c_int
+        if version() != ABI_VERSION:
+            raise RuntimeError(f"{LIBRARY} has ABI version {version()}, this binding "
+                               f"mirrors version {ABI_VERSION}; rebuild the library")
         for name, (args, ret) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes, fn.restype = args, ret
-        if lib.laya_abi_version() != ABI_VERSION:
-            raise RuntimeError(f"{LIBRARY} has ABI version {lib.laya_abi_version()}, this binding "
-                               f"mirrors version {ABI_VERSION}; rebuild the library")
         _lib = lib
     return _lib
 

@@ -39,6 +39,22 @@ def test_binding_refuses_a_library_of_another_abi_version(monkeypatch):
     assert _lib._lib is None  # nothing half-loaded is cached
 
 
+def test_binding_reports_the_version_of_a_library_missing_exports(monkeypatch):
+    """A library of another ABI that lacks the other exports fails on its version, not on a
+    missing symbol: the version is bound and compared before anything else is typed."""
+    def version():
+        return _lib.ABI_VERSION + 7
+
+    class OtherAbi:  # exports laya_abi_version only
+        laya_abi_version = staticmethod(version)
+
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib.ct, "CDLL", lambda path: OtherAbi())
+    with pytest.raises(RuntimeError, match=f"ABI version {_lib.ABI_VERSION + 7}"):
+        _lib.load()
+    assert _lib._lib is None
+
+
 def test_packed_block_size_matches_the_python_packer():
     from laya_cuda.runtime import pack
     lib = _lib.load()
