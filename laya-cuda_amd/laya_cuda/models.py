@@ -1,65 +1,67 @@
-"""JSON checkpoint configuration and a small model adapter registry (laya_cuda/models.py:1-58).
+"""Checkpoint location: a local directory, or an alias that a JSON registry maps to one.
 
-Local directories and ``{"path": ...}`` registry entries resolve as in the reference.  Entries
-pinned to a hosted ``repo_id``/``revision`` need a network download, which this build does not
-perform: they raise with a message naming the entry.
+The reference resolves aliases to hosted checkpoints and downloads them (laya_cuda/models.py:
+31-47).  This runtime never fetches anything: ``resolve`` accepts a checkpoint directory, or an
+alias from the ``registry`` file whose entry is ``{"path": dir}`` (relative paths are taken from
+the registry file's folder).  Entries naming a hosted ``repo_id``/``revision`` are recognised and
+refused with a message that says so.  Error types follow the reference: ``FileNotFoundError`` for
+unknown aliases and incomplete checkpoints, ``ValueError`` for a malformed registry.
 """
 import json
 from pathlib import Path
 
-FILES = ["model.safetensors", "rl_agent_config.json", "encoder/config.json", "tokenizer/*"]
+# Files a Laya checkpoint directory must hold (laya_cuda/models.py:6 lists them as download patterns).
+REQUIRED = ("model.safetensors", "rl_agent_config.json", "encoder/config.json", "tokenizer/tokenizer.json")
 
 
 def read_json(path):
     return json.loads(Path(path).read_text(encoding="utf-8"))
 
 
-def _checkpoints(registry=None):
-    sources = [Path(__file__).with_name("models.json")]
-    if registry is not None:
-        sources.append(Path(registry).expanduser())
-    entries = {}
-    for source in sources:
-        if not source.is_file():
-            continue
-        data = read_json(source)
-        if not isinstance(data, dict):
-            raise ValueError(f"Model registry must be a JSON object: {source}")
-        for alias, entry in data.items():
-            valid = (alias.strip() and isinstance(entry, dict)
-                     and set(entry) in ({"path"}, {"repo_id", "revision"})
-                     and all(isinstance(v, str) and v.strip() for v in entry.values()))
-            if not valid:
-                raise ValueError(f"Invalid model entry {alias!r} in {source}; use path or repo_id and revision")
-            if "path" in entry:
-                entry = {"path": str((source.parent / Path(entry["path"]).expanduser()).resolve())}
-            entries[alias] = entry
-    return entries
+def _text(value):
+    return isinstance(value, str) and bool(value.strip())
+
+
+def _lookup(alias, registry):
+    """The registry entry for ``alias`` ({"path": absolute} or {"repo_id", "revision"}), or None."""
+    if registry is None:
+        return None
+    source = Path(registry).expanduser()
+    table = read_json(source)  # FileNotFoundError / JSONDecodeError propagate
+    if not isinstance(table, dict):
+        raise ValueError(f"Model registry must be a JSON object: {source}")
+    found = None
+    for name, entry in table.items():
+        local = isinstance(entry, dict) and set(entry) == {"path"}
+        hosted = isinstance(entry, dict) and set(entry) == {"repo_id", "revision"}
+        if not (_text(name) and (local or hosted) and all(_text(v) for v in entry.values())):
+            raise ValueError(f"Invalid model entry {name!r} in {source}; use path or repo_id and revision")
+        if name == alias:
+            found = {"path": str((source.parent / Path(entry["path"]).expanduser()).resolve())} if local else entry
+    return found
 
 
 def resolve(model, revision=None, *, registry=None):
-    """Local checkpoint directory for ``model`` (a path or a registry alias)."""
-    path = Path(model).expanduser()
-    if not path.is_dir():
-        checkpoints = _checkpoints(registry)
-        if str(model) not in checkpoints:
+    """Absolute path of the checkpoint directory ``model`` names (a directory or a registry alias)."""
+    directory = Path(model).expanduser()
+    if not directory.is_dir():
+        entry = _lookup(str(model), registry)
+        if entry is None:
             raise FileNotFoundError(f"Unknown alias or missing local checkpoint: {model}")
-        entry = checkpoints[str(model)]
         if "path" not in entry:
             raise FileNotFoundError(
                 f"Alias {model!r} names hosted checkpoint {entry['repo_id']}@{revision or entry['revision']}; "
-                "download it and pass the local directory (this runtime does not fetch checkpoints)")
-        path = Path(entry["path"])
-    for name in FILES[:3] + ["tokenizer/tokenizer.json"]:
-        if not (path / name).is_file():
-            raise FileNotFoundError(f"Incomplete checkpoint: {path / name}")
-    return path.resolve()
+                "this runtime does not fetch checkpoints: download it and pass the local directory")
+        directory = Path(entry["path"])
+    missing = [name for name in REQUIRED if not (directory / name).is_file()]
+    if missing:
+        raise FileNotFoundError(f"Incomplete checkpoint: {directory / missing[0]}")
+    return directory.resolve()
 
 
 def adapter(path):
-    from .laya import Laya
-    registry = {"laya": Laya}
-    kind = "laya" if (path / "rl_agent_config.json").is_file() else None
-    if kind not in registry:
+    """The model adapter for a checkpoint directory (Laya checkpoints carry rl_agent_config.json)."""
+    if not (Path(path) / "rl_agent_config.json").is_file():
         raise ValueError("No compatible model adapter")
-    return registry[kind](path)
+    from .laya import Laya
+    return Laya(Path(path))
