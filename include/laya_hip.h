@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LAYA_ABI_VERSION 1
+#define LAYA_ABI_VERSION 2
 
 enum {
   LAYA_OK = 0,
@@ -197,6 +197,23 @@ int laya_op_qkv(const void* x, const void* w, const float* bias, void* q, void* 
 int laya_op_attention(const void* q, const void* k, const void* vt, void* out, const int32_t* tiles,
                       int m, int heads, int max_tiles, int mode, int waves, int window, int dtype16,
                       void* stream);
+
+/* gather / gather_half (kernels.cu:159-166), the option-position row gather of the decision head
+ * (laya.py:226-227, 237): for r < *n_live, dst32[r] = src32[indices[r]] and dst16[r] =
+ * src16[indices[r]] (16-bit rows of dtype16), bit-exact copies in the order of `indices`
+ * (duplicates allowed); rows n_live..rows-1 are written as zeros.  n_live is a device int32 (the
+ * forward reads the live row count on the device); either src/dst pair may be NULL to skip it. */
+int laya_op_gather_rows(const float* src32, float* dst32, const void* src16, void* dst16, int dtype16,
+                        const int32_t* indices, const int32_t* n_live, int rows, int width, void* stream);
+
+/* The scorer input rows (type_add + gather, kernels.cu:155-162; laya.py:236-238): for r < *n_live,
+ * selected[r] = src[src_rows[r]] + type_rows[question_kind[row_question[r]]] (the type row only
+ * when type_rows is non-NULL; one fp32 add, bit-exact), and normed[r] = LayerNorm(selected[r];
+ * gamma, beta, eps) (scorer.0).  All pointers are device memory; n_live a device int32. */
+int laya_op_head_gather(const float* src, const int32_t* src_rows, const int32_t* row_question,
+                        const int32_t* question_kind, const int32_t* n_live, const float* type_rows,
+                        const float* gamma, const float* beta, float eps, float* selected, float* normed,
+                        int rows, int width, void* stream);
 
 #ifdef __cplusplus
 }

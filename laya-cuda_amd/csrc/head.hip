@@ -45,20 +45,23 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherRowsArgs a) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= a.cap) return;
-  float v[D / 64];
   const bool live = r < *a.n;
   const int src = live ? a.idx[r] : 0;
-  if (live) {
-    load_row<D>(a.src32 + static_cast<size_t>(src) * D, lane, v);
-  } else {
+  if (a.src32) {
+    float v[D / 64];
+    if (live) {
+      load_row<D>(a.src32 + static_cast<size_t>(src) * D, lane, v);
+    } else {
 #pragma unroll
-    for (int i = 0; i < D / 64; ++i) v[i] = 0.f;
+      for (int i = 0; i < D / 64; ++i) v[i] = 0.f;
+    }
+    store_row<D>(a.dst32 + static_cast<size_t>(r) * D, lane, v);
   }
-  store_row<D>(a.dst32 + static_cast<size_t>(r) * D, lane, v);
-  // 16-bit rows: 8 elements (one 16-byte chunk) per lane per step.
-  const i32x4* s16 = reinterpret_cast<const i32x4*>(static_cast<const T*>(a.src16) + static_cast<size_t>(src) * D);
-  i32x4* d16 = reinterpret_cast<i32x4*>(static_cast<T*>(a.dst16) + static_cast<size_t>(r) * D);
-  for (int c = lane; c < D / 8; c += 64) d16[c] = live ? s16[c] : i32x4{0, 0, 0, 0};
+  if (a.src16) {  // 16-bit rows: 8 elements (one 16-byte chunk) per lane per step
+    const i32x4* s16 = reinterpret_cast<const i32x4*>(static_cast<const T*>(a.src16) + static_cast<size_t>(src) * D);
+    i32x4* d16 = reinterpret_cast<i32x4*>(static_cast<T*>(a.dst16) + static_cast<size_t>(r) * D);
+    for (int c = lane; c < D / 8; c += 64) d16[c] = live ? s16[c] : i32x4{0, 0, 0, 0};
+  }
 }
 
 // fp32 GEMM on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): parts[z] = X W^T over split z.

@@ -127,7 +127,8 @@ struct HeadGatherArgs {
 hipError_t launch_head_gather(const HeadGatherArgs& a, int width, hipStream_t stream);
 
 // Compact readout rows for the last head transformer layer: dst32[r] = src32[idx[r]] and
-// dst16[r] = src16[idx[r]] (bit-exact copies) for r < *n; rows n..cap-1 are zeroed.
+// dst16[r] = src16[idx[r]] (bit-exact copies) for r < *n; rows n..cap-1 are zeroed.  Either pair
+// may be null (that copy is skipped).
 struct GatherRowsArgs {
   const float* src32;
   float* dst32;

@@ -337,109 +337,122 @@ void destroy_slot(Engine& E, Slot* s) {
 // (at 512 rows the 16-bit form saves 8 us of add+LayerNorm per forward but costs 80 us of GEMM).
 constexpr int kBranch16Rows = 4096;
 
-Slot* create_slot(Engine& E, int m, int b, int k) {
+// Launch plans of a slot of shape (m, b, k): GEMM tiles and split-K, attention kernel, head
+// splits.  Host arithmetic only (no allocation).
+void plan_slot(const Engine& E, Slot* s, int m, int b, int k) {
   const LayaConfig& c = E.cfg;
-  Slot* s = new Slot();
   s->m = m;
   s->b = b;
   s->k = k;
   s->L = make_layout(m, b, k);
   const int d = c.width, f = c.intermediate;
-  try {
-    const int R = s->L.R;
-    gemm_plan(m, 3 * d, d, Epi::QKV, E.mfma(), E.cus, &s->tile[0], &s->splits[0], E.modern);
-    gemm_plan(m, d, d, Epi::F32, E.mfma(), E.cus, &s->tile[1], &s->splits[1]);
-    if (E.modern) {
-      gemm_plan(m, 2 * f, d, Epi::GEGLU, E.mfma(), E.cus, &s->tile[2], &s->splits[2]);
-    } else {
-      gemm_plan(m, f, d, Epi::GELU, E.mfma(), E.cus, &s->tile[2], &s->splits[2]);
-    }
-    gemm_plan(m, d, f, Epi::F32, E.mfma(), E.cus, &s->tile[3], &s->splits[3]);
-    s->splits[0] = s->splits[2] = 1;
-    if (m >= kBranch16Rows) {
-      s->branch16 = true;
-      gemm_plan(m, d, d, Epi::HALF, E.mfma(), E.cus, &s->tile[1], &s->splits[1]);
-      gemm_plan(m, d, f, Epi::HALF, E.mfma(), E.cus, &s->tile[3], &s->splits[3]);
-      s->splits[1] = s->splits[3] = 1;
-    }
-    if (E.modern) {  // head transformer layers: all rows, then the readout rows of the last one
-      gemm_plan(m, 3 * d, d, Epi::QKV, E.mfma(), E.cus, &s->htile[0], &s->hsplits[0]);
-      gemm_plan(m, d, d, Epi::F32, E.mfma(), E.cus, &s->htile[1], &s->hsplits[1]);
-      gemm_plan(m, 4 * d, d, Epi::RELU, E.mfma(), E.cus, &s->htile[2], &s->hsplits[2]);
-      gemm_plan(m, d, 4 * d, Epi::F32, E.mfma(), E.cus, &s->htile[3], &s->hsplits[3]);
-      gemm_plan(R, d, d, Epi::F32, E.mfma(), E.cus, &s->htile[4], &s->hsplits[4]);
-      gemm_plan(R, 4 * d, d, Epi::RELU, E.mfma(), E.cus, &s->htile[5], &s->hsplits[5]);
-      gemm_plan(R, d, 4 * d, Epi::F32, E.mfma(), E.cus, &s->htile[6], &s->hsplits[6]);
-      s->hsplits[0] = s->hsplits[2] = s->hsplits[5] = 1;
-    }
-    // Few 128-query tiles (batch-1 requests): split each tile's keys across waves instead of
-    // sharing LDS-staged keys between query tiles, so the serial key loop is short.
-    if (static_cast<long long>(m / 128) * c.heads >= 2LL * E.cus) {
-      s->attn_mode = kAttnSharedKV;
-      s->attn_waves = 8;
-    } else {
-      // Each 32-query tile's keys split across waves.  More waves shorten the serial key blocks
-      // per wave while the workgroups fit one round on the CUs (one workgroup per CU: four waves
-      // hold one per SIMD, eight two); at 512 tokens four waves measured 6.6 against 8.7 us for two
-      // (192 workgroups) and eight waves, one 64-key block each, 6.1 us, while at 1,024 tokens
-      // (384 workgroups) two waves, two workgroups per CU and one round win, 15.9 against 17.8 us.
-      s->attn_mode = kAttnSplitKeys;
-      const bool one_round = static_cast<long long>((m + 31) / 32) * c.heads <= E.cus;
-      s->attn_waves = !one_round ? 2 : m >= 8 * 64 ? 8 : 4;
-    }
-    // Tiles of at most `block` rows: every sequence, and every run of rows between or after
-    // sequences, adds at most one partial tile, so this bounds the work list of any request.
-    const int block = attention_block_rows(s->attn_mode, s->attn_waves);
-    s->attn_tiles = std::min(s->L.T, m / block + 2 * b + 1);
-    s->head_splits = head_gemm_splits(s->L.R, d, d, E.cus);
-    s->act_splits = head_gemm_splits(b, c.act_hidden, E.act_k, E.cus);
-    const int max_split = std::max(std::max(s->splits[1], s->splits[3]), std::max(s->hsplits[1], s->hsplits[3]));
-    const int sel_split = std::max(s->hsplits[4], s->hsplits[6]);
-    const size_t ff_cols = E.modern ? std::max(f, 4 * d) : f;  // GeGLU output f; head linear1 4d
+  gemm_plan(m, 3 * d, d, Epi::QKV, E.mfma(), E.cus, &s->tile[0], &s->splits[0], E.modern);
+  gemm_plan(m, d, d, Epi::F32, E.mfma(), E.cus, &s->tile[1], &s->splits[1]);
+  if (E.modern) {
+    gemm_plan(m, 2 * f, d, Epi::GEGLU, E.mfma(), E.cus, &s->tile[2], &s->splits[2]);
+  } else {
+    gemm_plan(m, f, d, Epi::GELU, E.mfma(), E.cus, &s->tile[2], &s->splits[2]);
+  }
+  gemm_plan(m, d, f, Epi::F32, E.mfma(), E.cus, &s->tile[3], &s->splits[3]);
+  s->splits[0] = s->splits[2] = 1;
+  if (m >= kBranch16Rows) {
+    s->branch16 = true;
+    gemm_plan(m, d, d, Epi::HALF, E.mfma(), E.cus, &s->tile[1], &s->splits[1]);
+    gemm_plan(m, d, f, Epi::HALF, E.mfma(), E.cus, &s->tile[3], &s->splits[3]);
+    s->splits[1] = s->splits[3] = 1;
+  }
+  const int R = s->L.R;
+  if (E.modern) {  // head transformer layers: all rows, then the readout rows of the last one
+    gemm_plan(m, 3 * d, d, Epi::QKV, E.mfma(), E.cus, &s->htile[0], &s->hsplits[0]);
+    gemm_plan(m, d, d, Epi::F32, E.mfma(), E.cus, &s->htile[1], &s->hsplits[1]);
+    gemm_plan(m, 4 * d, d, Epi::RELU, E.mfma(), E.cus, &s->htile[2], &s->hsplits[2]);
+    gemm_plan(m, d, 4 * d, Epi::F32, E.mfma(), E.cus, &s->htile[3], &s->hsplits[3]);
+    gemm_plan(R, d, d, Epi::F32, E.mfma(), E.cus, &s->htile[4], &s->hsplits[4]);
+    gemm_plan(R, 4 * d, d, Epi::RELU, E.mfma(), E.cus, &s->htile[5], &s->hsplits[5]);
+    gemm_plan(R, d, 4 * d, Epi::F32, E.mfma(), E.cus, &s->htile[6], &s->hsplits[6]);
+    s->hsplits[0] = s->hsplits[2] = s->hsplits[5] = 1;
+  }
+  // Few 128-query tiles (batch-1 requests): split each tile's keys across waves instead of
+  // sharing LDS-staged keys between query tiles, so the serial key loop is short.
+  if (static_cast<long long>(m / 128) * c.heads >= 2LL * E.cus) {
+    s->attn_mode = kAttnSharedKV;
+    s->attn_waves = 8;
+  } else {
+    // Each 32-query tile's keys split across waves.  More waves shorten the serial key blocks
+    // per wave while the workgroups fit one round on the CUs (one workgroup per CU: four waves
+    // hold one per SIMD, eight two); at 512 tokens four waves measured 6.6 against 8.7 us for two
+    // (192 workgroups) and eight waves, one 64-key block each, 6.1 us, while at 1,024 tokens
+    // (384 workgroups) two waves, two workgroups per CU and one round win, 15.9 against 17.8 us.
+    s->attn_mode = kAttnSplitKeys;
+    const bool one_round = static_cast<long long>((m + 31) / 32) * c.heads <= E.cus;
+    s->attn_waves = !one_round ? 2 : m >= 8 * 64 ? 8 : 4;
+  }
+  // Tiles of at most `block` rows: every sequence, and every run of rows between or after
+  // sequences, adds at most one partial tile, so this bounds the work list of any request.
+  const int block = attention_block_rows(s->attn_mode, s->attn_waves);
+  s->attn_tiles = std::min(s->L.T, m / block + 2 * b + 1);
+  s->head_splits = head_gemm_splits(s->L.R, d, d, E.cus);
+  s->act_splits = head_gemm_splits(b, c.act_hidden, E.act_k, E.cus);
+}
 
-    const size_t h2 = 2;  // 16-bit element
-    const size_t md = static_cast<size_t>(m) * d, Rz = R;
-    const size_t rows_sel = E.modern ? Rz : 0;  // compact head-layer buffers (ModernBERT only)
-    struct Part {
-      void** dst;
-      size_t bytes;
-    };
-    std::vector<Part> parts = {
-        {reinterpret_cast<void**>(&s->d_packed), s->L.total * 4},
-        {reinterpret_cast<void**>(&s->residual), md * 4},
-        {&s->x, md * h2},
-        {&s->q, md * h2},
-        {&s->kk, md * h2},
-        {&s->vt, md * h2},
-        {&s->attn, md * h2},
-        {&s->ff, static_cast<size_t>(m) * ff_cols * h2},
-        {reinterpret_cast<void**>(&s->part), md * 4 * max_split},
-        {reinterpret_cast<void**>(&s->selected), Rz * d * 4},
-        {reinterpret_cast<void**>(&s->normed), Rz * d * 4},
-        {reinterpret_cast<void**>(&s->hpart), Rz * d * 4 * s->head_splits},
-        {reinterpret_cast<void**>(&s->row_logit), Rz * 4},
-        {&s->attn_sel, rows_sel * d * h2},
-        {&s->x_sel, rows_sel * d * h2},
-        {&s->ff_sel, rows_sel * 4 * d * h2},
-        {reinterpret_cast<void**>(&s->part_sel), rows_sel * d * 4 * sel_split},
-        {reinterpret_cast<void**>(&s->feat), static_cast<size_t>(b) * E.act_k * 4},
-        {reinterpret_cast<void**>(&s->apart), static_cast<size_t>(b) * c.act_hidden * 4 * s->act_splits},
-        {reinterpret_cast<void**>(&s->logits), static_cast<size_t>(b) * (k + 1) * 4},
-        {reinterpret_cast<void**>(&s->acts), static_cast<size_t>(b) * c.n_act * 4},
-    };
-    size_t total = 0;
-    for (auto& p : parts) total += (p.bytes + 255) / 256 * 256;
+// The device buffers of a planned slot, in arena order, each starting at a 256-byte boundary.
+// Writes the buffer pointers relative to `base` (null: offsets only) and returns the arena size.
+size_t carve_slot(const Engine& E, Slot* s, char* base) {
+  const LayaConfig& c = E.cfg;
+  const int m = s->m, b = s->b, k = s->k, d = c.width, f = c.intermediate;
+  const int max_split = std::max(std::max(s->splits[1], s->splits[3]), std::max(s->hsplits[1], s->hsplits[3]));
+  const int sel_split = std::max(s->hsplits[4], s->hsplits[6]);
+  const size_t ff_cols = E.modern ? std::max(f, 4 * d) : f;  // GeGLU output f; head linear1 4d
+  const size_t h2 = 2;  // 16-bit element
+  const size_t md = static_cast<size_t>(m) * d, Rz = s->L.R;
+  const size_t rows_sel = E.modern ? Rz : 0;  // compact head-layer buffers (ModernBERT only)
+  struct Part {
+    void** dst;
+    size_t bytes;
+  };
+  const Part parts[] = {
+      {reinterpret_cast<void**>(&s->d_packed), s->L.total * 4},
+      {reinterpret_cast<void**>(&s->residual), md * 4},
+      {&s->x, md * h2},
+      {&s->q, md * h2},
+      {&s->kk, md * h2},
+      {&s->vt, md * h2},
+      {&s->attn, md * h2},
+      {&s->ff, static_cast<size_t>(m) * ff_cols * h2},
+      {reinterpret_cast<void**>(&s->part), md * 4 * max_split},
+      {reinterpret_cast<void**>(&s->selected), Rz * d * 4},
+      {reinterpret_cast<void**>(&s->normed), Rz * d * 4},
+      {reinterpret_cast<void**>(&s->hpart), Rz * d * 4 * s->head_splits},
+      {reinterpret_cast<void**>(&s->row_logit), Rz * 4},
+      {&s->attn_sel, rows_sel * d * h2},
+      {&s->x_sel, rows_sel * d * h2},
+      {&s->ff_sel, rows_sel * 4 * d * h2},
+      {reinterpret_cast<void**>(&s->part_sel), rows_sel * d * 4 * sel_split},
+      {reinterpret_cast<void**>(&s->feat), static_cast<size_t>(b) * E.act_k * 4},
+      {reinterpret_cast<void**>(&s->apart), static_cast<size_t>(b) * c.act_hidden * 4 * s->act_splits},
+      {reinterpret_cast<void**>(&s->logits), static_cast<size_t>(b) * (k + 1) * 4},
+      {reinterpret_cast<void**>(&s->acts), static_cast<size_t>(b) * c.n_act * 4},
+  };
+  size_t at = 0;
+  for (const Part& p : parts) {
+    *p.dst = base ? base + at : nullptr;
+    at += (p.bytes + 255) / 256 * 256;
+  }
+  return at;
+}
+
+Slot* create_slot(Engine& E, int m, int b, int k) {
+  Slot* s = new Slot();
+  try {
+    plan_slot(E, s, m, b, k);
+    const size_t total = carve_slot(E, s, nullptr);
     LAYA_HIP(hipMalloc(&s->arena, total));
     s->bytes = total;
     E.slot_bytes += total;
-    char* cur = static_cast<char*>(s->arena);
-    for (auto& p : parts) {
-      *p.dst = cur;
-      cur += (p.bytes + 255) / 256 * 256;
-    }
+    carve_slot(E, s, static_cast<char*>(s->arena));
     LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_packed), s->L.total * 4, hipHostMallocDefault));
     LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_logits), static_cast<size_t>(b) * (k + 1) * 4, hipHostMallocDefault));
-    LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_acts), static_cast<size_t>(b) * c.n_act * 4, hipHostMallocDefault));
+    LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_acts), static_cast<size_t>(b) * E.cfg.n_act * 4, hipHostMallocDefault));
     LAYA_HIP(hipEventCreate(&s->start));
     LAYA_HIP(hipEventCreate(&s->end));
   } catch (...) {
@@ -1291,6 +1304,33 @@ int laya_op_attention(const void* q, const void* k, const void* vt, void* out, c
     AttnArgs a{q, k, vt, out, tiles, m, heads, max_tiles, window < 0 ? -1 : window};
     check_launch(launch_attention(a, half_type(dtype16), mode, waves, static_cast<hipStream_t>(stream)),
                  "attention");
+  });
+}
+
+int laya_op_gather_rows(const float* src32, float* dst32, const void* src16, void* dst16, int dtype16,
+                        const int32_t* indices, const int32_t* n_live, int rows, int width, void* stream) {
+  return guarded(nullptr, [&] {
+    LAYA_REQUIRE(norm_width_supported(width), "unsupported width");
+    LAYA_REQUIRE(rows >= 0 && indices && n_live, "indices and the live row count are required");
+    LAYA_REQUIRE(!src32 == !dst32 && !src16 == !dst16, "each copy needs both its source and destination");
+    LAYA_REQUIRE(!src16 || dtype16 == LAYA_F16 || dtype16 == LAYA_BF16, "dtype16 must be LAYA_F16 or LAYA_BF16");
+    GatherRowsArgs a{src32, dst32, src16, dst16, indices, n_live, rows};
+    check_launch(launch_gather_rows(a, width, half_type(dtype16), static_cast<hipStream_t>(stream)), "gather rows");
+  });
+}
+
+int laya_op_head_gather(const float* src, const int32_t* src_rows, const int32_t* row_question,
+                        const int32_t* question_kind, const int32_t* n_live, const float* type_rows,
+                        const float* gamma, const float* beta, float eps, float* selected, float* normed,
+                        int rows, int width, void* stream) {
+  return guarded(nullptr, [&] {
+    LAYA_REQUIRE(norm_width_supported(width), "unsupported width");
+    LAYA_REQUIRE(rows >= 0 && src && src_rows && n_live && selected && normed && gamma && beta,
+                 "null argument");
+    LAYA_REQUIRE(!type_rows || (row_question && question_kind), "type rows need the question map and kinds");
+    HeadGatherArgs a{src, src_rows, row_question, question_kind, n_live, type_rows, gamma, beta, eps, selected,
+                     normed, rows};
+    check_launch(launch_head_gather(a, width, static_cast<hipStream_t>(stream)), "head gather");
   });
 }
 

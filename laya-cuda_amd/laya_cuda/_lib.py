@@ -9,7 +9,7 @@ from pathlib import Path
 LIBRARY = Path(__file__).with_name("liblaya_hip.so")
 
 OK, EINVAL, EDEVICE, ENOMEM, ESTATE = range(5)
-ABI_VERSION = 1  # LAYA_ABI_VERSION of the struct layouts mirrored below
+ABI_VERSION = 2  # LAYA_ABI_VERSION of the struct layouts mirrored below
 F32, F16, BF16 = 0, 1, 2
 NORM_POST, NORM_PRE = 0, 1
 POS_LEARNED, POS_ROPE = 0, 1
@@ -59,6 +59,8 @@ SIGNATURES = {
     "laya_op_linear": ([_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p], _i),
     "laya_op_qkv": ([_p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p], _i),
     "laya_op_attention": ([_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _p], _i),
+    "laya_op_gather_rows": ([_p, _p, _p, _p, _i, _p, _p, _i, _i, _p], _i),
+    "laya_op_head_gather": ([_p, _p, _p, _p, _p, _p, _p, _p, _f, _p, _p, _i, _i, _p], _i),
 }
 
 _lib = None

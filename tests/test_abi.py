@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     missing = [name for name in declared() if not hasattr(lib, name)]
     assert not missing
     assert set(declared()) <= set(_lib.SIGNATURES)
-    assert lib.laya_abi_version() == _lib.ABI_VERSION == 1
+    assert lib.laya_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_binding_refuses_a_library_of_another_abi_version(monkeypatch):

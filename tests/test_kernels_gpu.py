@@ -156,6 +156,82 @@ def test_norm_sums_split_partials_and_bias_in_order(gpu):
     np.testing.assert_array_equal(d_res.cpu().numpy(), res + (((parts[0] + parts[1]) + parts[2]) + bias))
 
 
+# ---------------- option-row gathers (decision head) ----------------
+
+@pytest.mark.parametrize("kind", ["f16", "bf16"])
+@pytest.mark.parametrize("width", [64, 768, 1024])
+def test_option_row_gather_is_bit_exact(gpu, kind, width):
+    """tests/test_gpu.py:106-112 of the reference: gathered rows keep the order of the indices,
+    duplicates included, bit for bit; here in fp32 and 16-bit at once, with rows past the live
+    count written as zeros."""
+    t = torch()
+    lib = _lib.load()
+    rng = np.random.default_rng(width)
+    values = rng.normal(0, 3, (40, width)).astype(np.float32)
+    values[5, :7] = [0.0, -0.0, np.inf, -np.inf, 1e-40, -3e38, 65504.0]  # signed zero, inf, subnormal
+    indices = np.array([0, 39, 3, 3, 1, 5, 39, 0, 22, 7, 7], np.int32)
+    live, rows = 9, len(indices)
+    half = t.float16 if kind == "f16" else t.bfloat16
+    src32 = dev(values, gpu)
+    src16 = dev(values, gpu).to(half)
+    dst32 = t.full((rows, width), float("nan"), device=gpu)
+    dst16 = t.full((rows, width), float("nan"), device=gpu).to(half)
+    d_idx, d_live = dev(indices, gpu), dev(np.array([live], np.int32), gpu)
+    check(lib.laya_op_gather_rows(p(src32), p(dst32), p(src16), p(dst16), DTYPES[kind][0], p(d_idx), p(d_live), rows,
+                                  width, stream()))
+    sync()
+    got32 = dst32.cpu().numpy()
+    np.testing.assert_array_equal(got32[:live].view(np.uint32), values[indices[:live]].view(np.uint32))
+    assert not got32[live:].view(np.uint32).any()
+    bits16 = src16.view(t.int16).cpu().numpy()
+    got16 = dst16.view(t.int16).cpu().numpy()
+    np.testing.assert_array_equal(got16[:live], bits16[indices[:live]])
+    assert not got16[live:].any()
+    # The 16-bit copy alone (the fp32 pair skipped): fp32 rows stay as they were.
+    dst32.fill_(7.0)
+    dst16.zero_()
+    check(lib.laya_op_gather_rows(None, None, p(src16), p(dst16), DTYPES[kind][0], p(d_idx), p(d_live), rows, width,
+                                  stream()))
+    sync()
+    np.testing.assert_array_equal(dst16.view(t.int16).cpu().numpy()[:live], bits16[indices[:live]])
+    assert (dst32.cpu().numpy() == 7.0).all()
+
+
+@pytest.mark.parametrize("width", [768, 1024])
+def test_head_gather_adds_type_rows_bit_exactly(gpu, width):
+    """type_add + gather (kernels.cu:155-162; laya.py:236-238): each scorer row is its packed
+    source row plus its question's type row, one fp32 add (bit-exact), then scorer.0's LayerNorm
+    (eps 1e-5).  Rows past the live count are not written."""
+    t = torch()
+    lib = _lib.load()
+    rng = np.random.default_rng(7)
+    residual = rng.normal(0, 1, (64, width)).astype(np.float32)
+    types = rng.normal(0, 1, (3, width)).astype(np.float32)
+    gamma, beta = rng.normal(1, .1, width).astype(np.float32), rng.normal(0, .1, width).astype(np.float32)
+    src_rows = np.array([0, 17, 17, 63, 2, 40, 0, 9], np.int32)      # CLS, options, ... (duplicates)
+    row_question = np.array([0, 0, 0, 0, 1, 1, 2, 2], np.int32)
+    question_kind = np.array([2, 0, 1], np.int32)
+    live, rows = 7, 8
+    selected = t.full((rows, width), float("nan"), device=gpu)
+    normed = t.full((rows, width), float("nan"), device=gpu)
+    args = [dev(a, gpu) for a in (residual, src_rows, row_question, question_kind, np.array([live], np.int32), types,
+                                  gamma, beta)]
+    check(lib.laya_op_head_gather(*[p(a) for a in args], 1e-5, p(selected), p(normed), rows, width, stream()))
+    sync()
+    want = residual[src_rows] + types[question_kind[row_question]]
+    got = selected.cpu().numpy()
+    np.testing.assert_array_equal(got[:live].view(np.uint32), want[:live].view(np.uint32))
+    np.testing.assert_allclose(normed.cpu().numpy()[:live], E.layer_norm(want[:live], gamma, beta, 1e-5),
+                               atol=2e-5, rtol=1e-5)
+    assert np.isnan(got[live:]).all() and np.isnan(normed.cpu().numpy()[live:]).all()
+    # Without type rows the scorer rows are plain copies.
+    check(lib.laya_op_head_gather(p(args[0]), p(args[1]), None, None, p(args[4]), None, p(args[6]), p(args[7]), 1e-5,
+                                  p(selected), p(normed), rows, width, stream()))
+    sync()
+    np.testing.assert_array_equal(selected.cpu().numpy()[:live].view(np.uint32),
+                                  residual[src_rows[:live]].view(np.uint32))
+
+
 # ---------------- MFMA GEMM ----------------
 
 def linear(x, w, bias, out, kind, dtype, M, N, K, splits, tile):

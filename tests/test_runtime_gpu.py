@@ -15,6 +15,10 @@ from laya_cuda.runtime import Runtime
 pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).resolve().parent / "golden"
 LOGIT_ATOL = 1e-3
+# Documented near-ties of the ragged 32-request workload: question 40's two best options are
+# 1.2e-5 apart in the oracle, well inside the logit error bound, so either order is a correct
+# reading of the same scores.  No other question may change its decision.
+RAGGED32_TIES = {40: 1.2e-5}
 
 
 def _cfg(spec):
@@ -26,29 +30,28 @@ def oracle_logits(spec, w, sequences, questions):
     return logits, acts
 
 
-def decisions(got_logits, want_logits, worst):
-    """(equal, near_ties): a decision may differ from the oracle's only on a near-tie, i.e. when
-    the oracle scores the GPU's choice within 2*worst of its own (two logits each off by at most
-    ``worst`` can swap order only then; e.g. ragged32 question 40 has options 1.2e-5 apart).
-    Anything else is a wrong decision."""
-    equal, ties = 0, []
+def decisions(got_logits, want_logits, worst, known_ties=()):
+    """Flipped decisions [(question, oracle gap)]: questions whose GPU argmax differs from the
+    oracle's.  Every flip must be a documented near-tie, listed in ``known_ties`` by question
+    index, whose oracle gap is within 2*worst (two logits each off by at most ``worst`` can swap
+    order only then).  Exact ties (duplicate option positions) give bit-identical logits on both
+    sides and break to the first index identically, so they never flip."""
+    flips = []
     for q, want in enumerate(want_logits):
         mine, theirs = int(np.argmax(got_logits[q, :len(want)])), int(np.argmax(want))
-        if mine == theirs:
-            equal += 1
-            continue
-        gap = float(want[theirs] - want[mine])
-        assert gap <= 2 * worst, f"question {q}: decision {mine} != {theirs} with oracle gap {gap:.3e}"
-        ties.append((q, gap))
-    return equal, ties
+        if mine != theirs:
+            flips.append((q, float(want[theirs] - want[mine])))
+    for q, gap in flips:
+        assert q in known_ties and gap <= 2 * worst, f"question {q}: decision differs, oracle gap {gap:.3e}"
+    return flips
 
 
-def compare(got_logits, got_acts, want_logits, want_acts, atol=LOGIT_ATOL, acts_atol=None):
+def compare(got_logits, got_acts, want_logits, want_acts, atol=LOGIT_ATOL, acts_atol=None, known_ties=(), label=""):
     worst = max(float(np.abs(got_logits[q, :len(w)] - w).max()) for q, w in enumerate(want_logits))
+    flips = decisions(got_logits, want_logits, worst, known_ties)
+    print(f"{label}: {len(want_logits) - len(flips)}/{len(want_logits)} decisions equal, flips {flips}, "
+          f"max |logit error| {worst:.3e}", flush=True)
     assert worst <= atol, f"max |logit error| {worst:.3e} > {atol}"
-    equal, ties = decisions(got_logits, want_logits, worst)
-    if ties:
-        print(f"{equal}/{len(want_logits)} decisions equal; near-ties (question, oracle gap): {ties}")
     np.testing.assert_allclose(got_acts, want_acts, atol=atol if acts_atol is None else acts_atol)
     return worst
 
@@ -64,9 +67,10 @@ def test_small_encoder_matches_golden_and_oracle(gpu):
     try:
         logits, acts, metrics = rt.predict_sequences(sequences, questions)
         golden = [g[f"q{q}_logits"] for q in range(len(questions))]
-        compare(logits, acts, golden, np.stack([g[f"q{q}_acts"] for q in range(len(questions))]), atol=5e-3)
+        compare(logits, acts, golden, np.stack([g[f"q{q}_acts"] for q in range(len(questions))]), atol=5e-3,
+                label="bert small vs transformers golden")
         want, want_acts = oracle_logits(spec, w, sequences, questions)
-        compare(logits, acts, want, want_acts, atol=5e-3)
+        compare(logits, acts, want, want_acts, atol=5e-3, label="bert small vs oracle")
         assert metrics["cache_miss"] and metrics["graph_capture"] and metrics["graph_replay"]
     finally:
         rt.close()
@@ -86,8 +90,7 @@ def test_workload_matches_oracle(gpu, name, dtype):
     rt = Runtime(spec, 0, 4, weights=w)
     try:
         logits, acts, _ = rt.predict_sequences(sequences, questions)
-        worst = compare(logits, acts, want, want_acts, atol=LOGIT_ATOL if dtype == "float16" else 2e-3)
-        print(f"{name} {dtype}: max |logit error| = {worst:.3e}")
+        compare(logits, acts, want, want_acts, atol=LOGIT_ATOL if dtype == "float16" else 2e-3, label=f"{name} {dtype}")
         eager = rt.predict_sequences(sequences, questions, capture=False)
         np.testing.assert_array_equal(eager[0], logits)
         np.testing.assert_array_equal(eager[1], acts)
@@ -103,8 +106,7 @@ def test_ragged_batch_matches_oracle(gpu):
     rt = Runtime(spec, 0, 4, weights=w)
     try:
         logits, acts, metrics = rt.predict_sequences(sequences, questions)
-        worst = compare(logits, acts, want, want_acts)
-        print(f"ragged32: {len(questions)} questions, max |logit error| = {worst:.3e}, shape {metrics['shape']}")
+        compare(logits, acts, want, want_acts, known_ties=RAGGED32_TIES, label=f"ragged32 {metrics['shape']}")
     finally:
         rt.close()
 
@@ -127,8 +129,8 @@ def test_batched_encoder_matches_oracle(gpu, dtype):
     try:
         logits, acts, metrics = rt.predict_sequences(sequences, questions)
         assert metrics["shape"][0] >= 4096, metrics["shape"]
-        worst = compare(logits, acts, want, want_acts, atol=LOGIT_ATOL if dtype == "float16" else 2e-3)
-        print(f"batched {dtype}: rows {metrics['shape'][0]}, max |logit error| = {worst:.3e}")
+        compare(logits, acts, want, want_acts, atol=LOGIT_ATOL if dtype == "float16" else 2e-3,
+                label=f"batched {dtype} rows {metrics['shape'][0]}")
     finally:
         rt.close()
 
@@ -146,7 +148,7 @@ def test_reference_items_each_question_its_own_row(gpu):
         logits, acts, metrics = rt.predict(items)
         assert metrics["shape"] == (128, 4, 8)
         want, want_acts = oracle_logits(spec, w, [i[0] for i in items], [(q, i[1], i[2]) for q, i in enumerate(items)])
-        compare(logits, acts, want, want_acts)
+        compare(logits, acts, want, want_acts, label="reference items")
     finally:
         rt.close()
 
@@ -244,9 +246,10 @@ def test_modernbert_small_matches_golden_and_oracle(gpu, dtype):
         logits, acts, metrics = rt.predict(items)
         atol, acts_atol = (3e-2, 0.4) if dtype == "float16" else (0.3, 2.5)
         golden = [g[f"q{q}_logits"] for q in range(len(items))]
-        compare(logits, acts, golden, np.stack([g[f"q{q}_acts"] for q in range(len(items))]), atol, acts_atol)
+        compare(logits, acts, golden, np.stack([g[f"q{q}_acts"] for q in range(len(items))]), atol, acts_atol,
+                label=f"modernbert small {dtype} vs transformers golden")
         want, want_acts = _modern_oracle(spec, w, items)
-        compare(logits, acts, want, want_acts, atol, acts_atol)
+        compare(logits, acts, want, want_acts, atol, acts_atol, label=f"modernbert small {dtype} vs oracle")
         assert metrics["graph_capture"] and metrics["graph_replay"]
         eager = rt.predict(items, capture=False)
         np.testing.assert_array_equal(eager[0], logits)
@@ -273,8 +276,8 @@ def test_modernbert_small_at_checkpoint_scale_matches_oracle(gpu, dtype):
     rt = Runtime(spec, 0, 2, weights=w)
     try:
         logits, acts, _ = rt.predict(items)
-        worst = compare(logits, acts, want, want_acts, atol=LOGIT_ATOL if dtype == "float16" else 2e-3)
-        print(f"modernbert small {dtype}: max |logit error| = {worst:.3e}")
+        compare(logits, acts, want, want_acts, atol=LOGIT_ATOL if dtype == "float16" else 2e-3,
+                label=f"modernbert small {dtype} at checkpoint scale")
     finally:
         rt.close()
 
@@ -292,8 +295,7 @@ def test_modernbert_base_shaped_encoder_matches_oracle(gpu):
     rt = Runtime(spec, 0, 2, weights=w)
     try:
         logits, acts, _ = rt.predict(items)
-        worst = compare(logits, acts, want, want_acts)
-        print(f"modernbert 6L/768: max |logit error| = {worst:.3e}")
+        compare(logits, acts, want, want_acts, label="modernbert 6L/768")
     finally:
         rt.close()
 
