@@ -113,6 +113,20 @@ int laya_finalize(void* handle);
 int laya_predict(void* handle, const int32_t* host_packed, const LayaShape* shape, int capture,
                  float* host_logits, float* host_acts, LayaMetrics* metrics);
 
+/* No counterpart in the reference.  For callers that cannot allocate device or pinned memory
+ * (tight serving loops, harnesses that forbid hipMalloc): the forward of laya_predict without a
+ * shape slot.  Its arena (packed block, activations, split-K partials, head buffers) lives in a
+ * fixed 64 MiB device array that every device running the library holds for the life of the
+ * process; the packed block is staged through a fixed host array of 2^18 int32.  A shape class
+ * whose arena or block does not fit is refused with LAYA_EINVAL (12L/768 requests of up to 1,024
+ * packed rows fit).  The forward runs eagerly on the engine's stream (no graph), outputs and
+ * metrics as laya_predict (cache_miss, graph_capture and graph_replay are 0).  The call makes no
+ * allocation.  Calls share each device's array and the host staging: the library serialises them
+ * with a process-wide lock, held until the outputs are on the host; calls that overlapped would
+ * race on the array, and each call overwrites what the previous one left there. */
+int laya_predict_static(void* handle, const int32_t* host_packed, const LayaShape* shape, float* host_logits,
+                        float* host_acts, LayaMetrics* metrics);
+
 /* Per-launch timing, the native counterpart of the reference's profiling hook that records events
  * around every Ops.call/linear (tools/profile_long.py:21-67).  The forward is a fixed list of
  * stages (embed_norm; per layer qkv, attention, attn_out, attn_norm, ffn_up, ffn_down, ffn_norm;

@@ -22,6 +22,13 @@
 #include "kernels.hpp"
 #include "laya_hip.h"
 
+// Device scratch of laya_predict_static: the whole shape-slot arena of one forward (packed block,
+// activations, split-K partials, head buffers) for callers that cannot allocate.  The loader gives
+// every device that runs this library its own copy, held until the process ends; host code takes
+// its address per device with hipGetSymbolAddress (prepare_device) and never uses this name.
+constexpr size_t kScratchBytes = static_cast<size_t>(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 namespace laya {
 namespace {
 
@@ -203,6 +210,7 @@ struct Engine {
   float* a0w_pad = nullptr;  // act_head.0 weight [act_hidden][act_k], zero columns past d+4
   int act_k = 0;
   std::list<Slot*> lru;  // front = least recently used
+  hipEvent_t static_start = nullptr, static_end = nullptr;  // timing of laya_predict_static
   std::string error;
 
   DType mfma() const { return cfg.mfma_dtype == LAYA_F16 ? DType::F16 : DType::BF16; }
@@ -858,15 +866,30 @@ int guarded(Engine* E, F&& body) {
 
 std::mutex g_prepare_mutex;
 std::vector<int> g_prepared;
+// Per device: the device address of `scratch` (each device holds its own copy of the array).
+constexpr int kMaxDevices = 64;
+void* g_scratch[kMaxDevices] = {};
+// One-time set-up of the current device: GEMM kernel attributes and the scratch address.
 void prepare_device() {
   int dev = 0;
   LAYA_HIP(hipGetDevice(&dev));
   std::lock_guard<std::mutex> lock(g_prepare_mutex);
   for (int d : g_prepared)
     if (d == dev) return;
+  LAYA_REQUIRE(dev >= 0 && dev < kMaxDevices, "device index beyond the library's device table");
   LAYA_HIP(gemm_prepare());
+  void* ptr = nullptr;
+  LAYA_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  LAYA_REQUIRE(ptr != nullptr, "no device address for the scratch array");
+  g_scratch[dev] = ptr;
   g_prepared.push_back(dev);
 }
+
+// laya_predict_static: host staging of the packed block (pageable, process-wide) and the lock
+// that serialises the calls, which share each device's scratch.
+constexpr size_t kStaticStageInts = static_cast<size_t>(1) << 18;
+int32_t g_static_stage[kStaticStageInts];
+std::mutex g_static_mutex;
 
 }  // namespace
 }  // namespace laya
@@ -905,9 +928,13 @@ int laya_create(const LayaConfig* cfg, int device, int max_slots, void** handle)
     E->modern = cfg->norm_order == LAYA_NORM_PRE;
     prepare_device();
     LAYA_HIP(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
+    LAYA_HIP(hipEventCreate(&E->static_start));
+    LAYA_HIP(hipEventCreate(&E->static_end));
     build_expected(*E);
   });
   if (rc != LAYA_OK) {
+    if (E->static_start) (void)hipEventDestroy(E->static_start);
+    if (E->static_end) (void)hipEventDestroy(E->static_end);
     if (E->stream) (void)hipStreamDestroy(E->stream);
     delete E;
     return rc;
@@ -1119,6 +1146,54 @@ int laya_predict(void* handle, const int32_t* host_packed, const LayaShape* shap
   });
 }
 
+int laya_predict_static(void* handle, const int32_t* host_packed, const LayaShape* shape, float* host_logits,
+                        float* host_acts, LayaMetrics* metrics) {
+  Engine* E = static_cast<Engine*>(handle);
+  if (!E) return fail(nullptr, Failure{LAYA_EINVAL, "null handle"});
+  return guarded(E, [&] {
+    if (!E->finalized) throw Failure{LAYA_ESTATE, "predict before laya_finalize"};
+    LAYA_REQUIRE(host_packed && shape && host_logits && host_acts, "null argument");
+    const int m = shape->rows, b = shape->batch, k = shape->options;
+    LAYA_REQUIRE(m > 0 && m % 16 == 0 && m <= (1 << 22) && b > 0 && b <= (1 << 16) && k > 0 && k <= (1 << 12),
+                 "invalid shape class");
+    Slot s;  // plans and views into the scratch; owns nothing
+    plan_slot(*E, &s, m, b, k);
+    const size_t need = carve_slot(*E, &s, nullptr);
+    LAYA_REQUIRE(need <= kScratchBytes,
+                 "shape class (" + std::to_string(m) + ", " + std::to_string(b) + ", " + std::to_string(k) +
+                     ") needs " + std::to_string(need) + " bytes of device scratch; laya_predict_static holds " +
+                     std::to_string(kScratchBytes) + " (use laya_predict)");
+    LAYA_REQUIRE(s.L.total <= kStaticStageInts, "packed block exceeds the static staging buffer (use laya_predict)");
+    LAYA_HIP(hipSetDevice(E->device));
+    char* base = static_cast<char*>(g_scratch[E->device]);
+    LAYA_REQUIRE(base != nullptr, "device scratch not set up");
+    std::lock_guard<std::mutex> lock(g_static_mutex);
+    carve_slot(*E, &s, base);
+    s.h_packed = g_static_stage;
+    std::memcpy(s.h_packed, host_packed, s.L.user_end * 4);
+    derive_inputs(*E, s);
+    LAYA_HIP(hipMemcpyAsync(s.d_packed, s.h_packed, s.L.total * 4, hipMemcpyHostToDevice, E->stream));
+    LAYA_HIP(hipEventRecord(E->static_start, E->stream));
+    forward(*E, s);
+    LAYA_HIP(hipEventRecord(E->static_end, E->stream));
+    // logits: option slots 1..k of each question's row (laya.py:208), straight into the caller's rows
+    LAYA_HIP(hipMemcpy2DAsync(host_logits, static_cast<size_t>(k) * 4, s.logits + 1, static_cast<size_t>(k + 1) * 4,
+                              static_cast<size_t>(k) * 4, b, hipMemcpyDeviceToHost, E->stream));
+    LAYA_HIP(hipMemcpyAsync(host_acts, s.acts, static_cast<size_t>(b) * E->cfg.n_act * 4, hipMemcpyDeviceToHost,
+                            E->stream));
+    LAYA_HIP(hipStreamSynchronize(E->stream));
+    float ms = 0.f;
+    LAYA_HIP(hipEventElapsedTime(&ms, E->static_start, E->static_end));
+    if (metrics) {
+      metrics->gpu_ms = ms;
+      metrics->cache_miss = 0;
+      metrics->graph_capture = 0;
+      metrics->graph_replay = 0;
+      metrics->owned_gpu_bytes = static_cast<int64_t>(E->weight_bytes + E->slot_bytes);
+    }
+  });
+}
+
 int laya_stage_count(void) { return kStageCount; }
 
 const char* laya_stage_name(int stage) { return stage >= 0 && stage < kStageCount ? kStageNames[stage] : nullptr; }
@@ -1207,6 +1282,8 @@ int laya_destroy(void* handle) {
   E->weights.clear();
   if (E->a0w_pad) (void)hipFree(E->a0w_pad);
   if (E->rope) (void)hipFree(E->rope);
+  if (E->static_start) (void)hipEventDestroy(E->static_start);
+  if (E->static_end) (void)hipEventDestroy(E->static_end);
   if (E->stream) (void)hipStreamDestroy(E->stream);
   delete E;
   return LAYA_OK;

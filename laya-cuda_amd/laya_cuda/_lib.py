@@ -43,6 +43,7 @@ SIGNATURES = {
     "laya_load_weight": ([_p, ct.c_char_p, _p, _i, ct.POINTER(_i64), _i], _i),
     "laya_finalize": ([_p], _i),
     "laya_predict": ([_p, _ip, ct.POINTER(LayaShape), _i, _fp, _fp, ct.POINTER(LayaMetrics)], _i),
+    "laya_predict_static": ([_p, _ip, ct.POINTER(LayaShape), _fp, _fp, ct.POINTER(LayaMetrics)], _i),
     "laya_stage_count": ([], _i),
     "laya_stage_name": ([_i], ct.c_char_p),
     "laya_time_stage": ([_p, _ip, ct.POINTER(LayaShape), _i, _i, _i, _fp], _i),
