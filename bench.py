@@ -1,35 +1,40 @@
 """Benchmark of the MI355X encoder forward path behind Runtime.predict (one GPU).
 
-    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 15] [--extras]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--cpu-seconds 15] [--only NAMES] [--eager]
 
-Headline workload (one JSON line on stdout): the 12-layer, d=768, 12-head, FFN 3072 post-LN
-encoder with fp32 weights resident as fp16 MFMA operands (fp32 accumulate), one 512-token sequence
-carrying two questions (4 and 6 options).  fp16 rather than bf16 operands: with bf16 the logits
-move by 1.4e-3 from the FP32 path (over the 1e-3 bound), with fp16 by about 2e-4.  A step is one
-``predict`` of that request: packed upload, hipGraph replay of the whole forward (embedding gather + LayerNorm, 12 x [QKV GEMM, attention, out GEMM,
-add+LN, FFN up GEMM+GELU, FFN down GEMM, add+LN], option gather, scorer, per-question softmax,
-act head) and read-back of logits and acts.
+One JSON line on stdout.  Headline (`value`): the 512-token workload - the 12-layer, d=768,
+12-head, FFN 3072 post-LN encoder with fp32 weights resident as fp16 MFMA operands (fp32
+accumulate), one 512-token sequence carrying two questions (4 and 6 options).  fp16 rather than
+bf16 operands: with bf16 the logits move by 1.4e-3 from the FP32 path (over the 1e-3 bound), with
+fp16 by about 2e-4.  A step is one `predict` of the request: packed upload, hipGraph replay of the
+whole forward, read-back of logits and acts.
 
-Fields:
-  value / p95_ms        p50 / p95 of the forward's device time (events around the graph replay,
-                        inputs already resident in HBM), ms
-  predict_p50/p95_ms    the whole predict call seen by the caller (packing, H2D, replay, D2H)
-  ms_per_step           wall time of the timed loop / steps
-  first_ms              the first predict of the shape (slot allocation + hipGraph capture)
-  roofline              the kernel with the largest share of the forward, timed live with HIP
-                        events over back-to-back launches on the engine's stream
-  cpu_baseline          the NumPy FP32 restatement of the same forward on this host's cores
-  parity                GPU logits vs that CPU forward: max |logit error|, decisions equal
-``--calibrate-copy`` first runs a 64 MiB device copy (the reference for the HBM byte counters of a
-``rocprofv3 --pmc`` run).  ``--eager`` launches the forward kernel by kernel instead of replaying its hipGraph (for
-profilers that cannot follow graph launches).  ``--extras`` adds the other workloads: 83- and 1,024-token latency, the 32-request ragged batch
-(sequences/s) and the 24-layer d=1024 64 x 1024 batch (sequences/s and MFMA utilisation);
-``--workloads`` picks a subset of them.
+Every workload of the metric is measured in the same run, under `workloads`:
+  l83        same encoder, 83 tokens, one 4-option question              p50/p95 latency
+  l1024      12L/768, 250,002-row vocabulary, 1,024 Zipf tokens, 3x5      p50/p95 latency
+  ragged32   32 requests of 40-900 tokens, 1-5 questions of 4-77 options  sequences/s
+  b64x1024   24L/1024, 16 heads, bf16, 64 x 1,024 tokens, 8 options each  sequences/s, MFMA fraction
+and two host-inclusive measurements:
+  engine_predict_l512  Engine.predict on a synthetic checkpoint with a tokenizer: tokenise, pack,
+                       forward, decode (the reference's definition of predict latency)
+  batching             Engine serialised behind a lock vs BatchEngine, closed-loop clients
+                       (1/8/32 in flight), latency percentiles, requests/s, slot-cache misses
+
+Per workload: p50/p95 of the forward's device time (events around the graph replay; inputs
+resident in HBM) and of the whole predict call (packing, H2D, replay, D2H); first_ms (slot
+allocation + graph capture); per-stage device time per forward, each stage timed where it runs
+(every kernel of the stage inside eager forwards records its own start and end events, the
+interval a kernel trace reports); `roofline` of the stage with the
+largest share; `cpu_baseline` (the NumPy FP32 oracle of the same forward on this host's cores) and
+`parity` (GPU logits against that CPU forward).
 """
 import argparse
 import json
 import os
+import shutil
 import sys
+import tempfile
+import threading
 import time
 from pathlib import Path
 
@@ -42,17 +47,35 @@ sys.path.insert(0, str(ROOT))
 METRIC = "p50/p95 predict latency (ms) at 83/512/1024 tok; seqs/sec at batch 32"
 MFMA_PEAK_TFLOPS = 2500.0   # MI355X dense bf16/fp16
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+TRAFFIC = ROOT / "profiles" / "traffic.json"
+
+# name: (MFMA operand type, text of the workload)
+WORKLOADS = {
+    "l512": ("float16", "12-layer post-LN encoder d=768, 12 heads x 64, FFN 3072 GELU, vocab 50368, batch 1 x 512 "
+                        "tokens, 2 questions (4 and 6 options), fp32 weights resident as fp16 MFMA operands, fp32 "
+                        "accumulate"),
+    "l83": ("float16", "same 12L/768 encoder, batch 1 x 83 tokens, one 4-option question, fp16 operands"),
+    "l1024": ("float16", "12L/768 encoder, vocab 250,002 (768 MB fp32 table), 1,024 positions, batch 1 x 1,024 "
+                         "Zipf(1.1) tokens, 3 questions x 5 options, fp16 operands"),
+    "ragged32": ("float16", "12L/768 encoder, 32 requests of U{40..900} tokens packed back to back, 1-5 questions "
+                            "of 4-77 options each, fp16 operands"),
+    "b64x1024": ("bfloat16", "24-layer post-LN encoder d=1024, 16 heads x 64, FFN 4096 GELU, bf16 weights and "
+                             "operands, 64 x 1,024 dense tokens, one 8-option question per sequence"),
+}
 
 
 def pct(values, q):
     return float(np.percentile(np.asarray(values, np.float64), q))
 
 
-def stage_work(stage, spec, lengths):
-    """Algorithmic work of ONE launch of a stage: ("mfma", FLOP) or ("hbm", bytes).
+def progress(message):
+    print(f"bench: {message}", file=sys.stderr, flush=True)
 
-    Valid tokens only.  GEMMs 2*T*N*K; attention 4*L^2*d per sequence (QK^T and PV);
-    embedding gather + LN T*(4 + 14d) + 8d bytes; residual add + LN 12*T*d bytes."""
+
+def stage_work(stage, spec, lengths):
+    """Algorithmic work of ONE launch of a stage: ("mfma", FLOP) or ("hbm", bytes), valid tokens only.
+    GEMMs 2*T*N*K; attention 4*L^2*d per sequence (QK^T and PV); embedding gather + LN
+    T*(4 + 14d) + 8d bytes; residual add + LN 12*T*d bytes."""
     d, f = spec.width, spec.intermediate
     T = sum(lengths)
     if stage == "qkv":
@@ -70,14 +93,29 @@ def stage_work(stage, spec, lengths):
     return None, 0.0
 
 
-def progress(message):
-    print(f"bench: {message}", file=sys.stderr, flush=True)
+def blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        return max([int(i.get("num_threads", 1)) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        return len(os.sched_getaffinity(0))
 
 
-def time_workload(rt, sequences, questions, steps, warmup, capture=True):
-    first = time.perf_counter()
+def measured_traffic(workload, stage):
+    """HBM bytes per launch of `stage` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    (copy-kernel calibrated), when they cover this workload and stage."""
+    try:
+        data = json.loads(TRAFFIC.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = data.get(workload, {}).get("stages", {}).get(stage)
+    return None if entry is None else entry.get("bytes_per_launch")
+
+
+def time_predict(rt, sequences, questions, steps, warmup, capture):
+    start = time.perf_counter()
     rt.predict_sequences(sequences, questions, capture)
-    first_ms = (time.perf_counter() - first) * 1e3
+    first_ms = (time.perf_counter() - start) * 1e3
     for _ in range(warmup):
         rt.predict_sequences(sequences, questions, capture)
     gpu, api = [], []
@@ -92,253 +130,249 @@ def time_workload(rt, sequences, questions, steps, warmup, capture=True):
 
 
 def stage_profile(rt, spec, sequences, questions, reps):
+    """Per stage: average device time of one launch where it runs (start/end events of every
+    kernel of the stage inside `reps` eager forwards), launches per forward and algorithmic work."""
     lengths = [len(s) for s in sequences]
     rows = []
     for name in rt.stages():
-        n, layer = rt.stage_launches(name)
+        n, _ = rt.stage_launches(name)
         if n == 0:
             continue
-        ms = rt.time_stage(sequences, questions, name, layer, reps)
+        ms = rt.time_stage(sequences, questions, name, -1, reps)
         bound, work = stage_work(name, spec, lengths)
         rows.append(dict(stage=name, ms=ms, launches=n, forward_ms=ms * n, bound=bound, work=work))
     return rows
 
 
-def roofline(row):
+def roofline(row, workload):
+    rate = row["work"] / (row["ms"] * 1e-3)
     if row["bound"] == "mfma":
-        achieved = row["work"] / (row["ms"] * 1e-3) / 1e12
-        return {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(achieved / MFMA_PEAK_TFLOPS, 4), "traffic": None, "kernel": row["stage"],
-                "avg_launch_us": round(row["ms"] * 1e3, 2), "work_per_launch": row["work"]}
-    achieved = row["work"] / (row["ms"] * 1e-3) / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": row["stage"],
-            "avg_launch_us": round(row["ms"] * 1e3, 2), "work_per_launch": row["work"]}
+        achieved, peak, unit = rate / 1e12, MFMA_PEAK_TFLOPS, "TFLOP/s"
+    else:
+        achieved, peak, unit = rate / 1e9, HBM_PEAK_GBS, "GB/s"
+    return {"bound": row["bound"], "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": measured_traffic(workload, row["stage"]),
+            "kernel": row["stage"], "avg_launch_us": round(row["ms"] * 1e3, 3), "work_per_launch": row["work"],
+            "timing": "start/end events of every kernel of the stage inside eager forwards (hipExtLaunchKernel, engine stream)"}
 
 
-def cpu_baseline(spec, weights, sequences, questions, seconds):
-    """The oracle's FP32 forward of the same request, repeated for about ``seconds``."""
+def oracle_forward(spec, weights, sequences, questions):
     import oracle.encoder as E
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([int(i.get("num_threads", 1)) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:
-        threads = len(os.sched_getaffinity(0))
     cfg = {"width": spec.width, "heads": spec.heads, "eps": spec.eps, "layers": spec.layers}
     w = E.structured(weights, cfg)
-    out = E.forward(sequences, questions, w, cfg)  # warm-up, and the parity reference
-    times = []
+    return lambda: E.forward(sequences, questions, w, cfg)
+
+
+def cpu_baseline(run, seconds, most=50):
+    """Time `run` (the oracle's FP32 forward) for about `seconds` (at least once); returns
+    (times in ms, the last output).  The first call is a warm-up unless it alone took over 2 s
+    (then it is the first sample)."""
+    s = time.perf_counter()
+    out = run()
+    first = (time.perf_counter() - s) * 1e3
+    times = [first] if first > 2000 else []
     start = time.perf_counter()
-    while not times or (time.perf_counter() - start < seconds and len(times) < 50):
+    while not times or (time.perf_counter() - start < seconds and len(times) < most):
         s = time.perf_counter()
-        E.forward(sequences, questions, w, cfg)
+        out = run()
         times.append((time.perf_counter() - s) * 1e3)
-    return times, threads, out
+    return times, out
 
 
-TRAFFIC = ROOT / "profiles" / "traffic.json"
+def parity(got_logits, got_acts, want_logits, want_acts):
+    worst = max(float(np.abs(got_logits[q, :len(w)] - w).max()) for q, w in enumerate(want_logits))
+    flips = [q for q, w in enumerate(want_logits) if int(np.argmax(got_logits[q, :len(w)])) != int(np.argmax(w))]
+    return {"max_abs_logit_err": worst, "max_abs_act_err": float(np.abs(got_acts - want_acts).max()),
+            "questions": len(want_logits), "decisions_differing": flips}
 
 
-def measured_traffic(stage):
-    """HBM bytes per launch of ``stage`` at the 512-token workload, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes (profiles/traffic.json, copy-kernel calibrated), if they cover it."""
-    try:
-        data = json.loads(TRAFFIC.read_text())
-    except (OSError, ValueError):
-        return None
-    entry = data.get("stages", {}).get(stage)
-    return None if entry is None else entry.get("bytes_per_launch")
-
-
-def calibrate_copy():
-    """A plain device-to-device copy of 64 MiB, three times: the known-size reference that scales
-    the FETCH_SIZE and WRITE_SIZE counters of the same profiler run."""
-    import torch
-    src = torch.ones(16 << 20, dtype=torch.float32, device="cuda:0")
-    dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    del src, dst
-
-
-def run_headline(args):
+def run_workload(name, args):
+    """Timing, stage profile, roofline, CPU baseline and parity of one workload."""
     from laya_cuda import synthetic
     from laya_cuda.runtime import Runtime
 
-    if args.calibrate_copy:
-        calibrate_copy()
-        progress("copy calibration done")
-
-    spec = synthetic.adapter("l512", mfma_dtype="float16")
-    weights = synthetic.weights(spec, seed=0)
-    sequences, questions = synthetic.request("l512", seed=1)
-    rt = Runtime(spec, 0, 4, weights=weights)
+    dtype, text = WORKLOADS[name]
+    spec = synthetic.adapter(name, mfma_dtype=dtype)
+    weights = synthetic.weights(spec, seed=0, bf16=synthetic.WORKLOADS[name].get("bf16", False))
+    sequences, questions = synthetic.request(name, seed=1)
+    lengths = [len(s) for s in sequences]
+    heavy = name in ("ragged32", "b64x1024")
+    steps = args.steps if not heavy else max(5, args.steps // 2) if name == "ragged32" else max(3, args.steps // 4)
+    warmup = args.warmup if not heavy else min(args.warmup, 3)
+    rt = Runtime(spec, 0, 2, weights=weights)
     try:
-        _sync()
-        r = time_workload(rt, sequences, questions, args.steps, args.warmup, not args.eager)
-        _sync()
-        progress(f"l512 timed: p50 {pct(r['gpu'], 50):.4f} ms")
-        rows = stage_profile(rt, spec, sequences, questions, args.stage_reps)
-        progress("stage timings done")
+        r = time_predict(rt, sequences, questions, steps, warmup, not args.eager)
+        progress(f"{name}: p50 {pct(r['gpu'], 50):.4f} ms device, {pct(r['api'], 50):.4f} ms predict")
+        rows = stage_profile(rt, spec, sequences, questions, 2 if heavy else args.stage_reps)
+        progress(f"{name}: stage timings done")
     finally:
         rt.close()
+    p50 = pct(r["gpu"], 50)
+    flops = synthetic.valid_flops(spec, lengths)
     dominant = max((row for row in rows if row["bound"]), key=lambda row: row["forward_ms"])
-    line = {
-        "metric": METRIC, "value": round(pct(r["gpu"], 50), 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(r["wall"] * 1e3 / args.steps, 4), "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
-        "config": {"workload": "l512: 12-layer post-LN encoder d=768, 12 heads x 64, FFN 3072 GELU, vocab 50368, "
-                               "batch 1 x 512 tokens, 2 questions (4 and 6 options), fp32 weights resident as "
-                               "fp16 MFMA operands, fp32 accumulate", "seq_len": 512, "global_batch": 1,
-                   "parallelism": "single GPU"},
-        "p95_ms": round(pct(r["gpu"], 95), 4),
-        "predict_p50_ms": round(pct(r["api"], 50), 4), "predict_p95_ms": round(pct(r["api"], 95), 4),
-        "first_ms": round(r["first_ms"], 3), "graph_replay": not args.eager,
-        "tflops_forward": round(synthetic.valid_flops(spec, [512]) / (pct(r["gpu"], 50) * 1e-3) / 1e12, 2),
-        "roofline": dict(roofline(dominant), traffic=measured_traffic(dominant["stage"])),
-        "stages_us_per_forward": {row["stage"]: round(row["forward_ms"] * 1e3, 2) for row in rows},
-    }
+    out = {"workload": text, "dtype": "f16" if dtype == "float16" else "bf16", "steps": steps, "warmup": warmup,
+           "p50_ms": round(p50, 4), "p95_ms": round(pct(r["gpu"], 95), 4),
+           "predict_p50_ms": round(pct(r["api"], 50), 4), "predict_p95_ms": round(pct(r["api"], 95), 4),
+           "ms_per_step": round(r["wall"] * 1e3 / steps, 4), "first_ms": round(r["first_ms"], 3),
+           "graph_replay": bool(r["metrics"]["graph_replay"]), "shape": list(r["metrics"]["shape"]),
+           "valid_tokens": int(sum(lengths)), "gflop_forward": round(flops / 1e9, 2),
+           "tflops_forward": round(flops / (p50 * 1e-3) / 1e12, 2),
+           "mfma_frac_forward": round(flops / (p50 * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+           "roofline": roofline(dominant, name),
+           "stages_us_per_forward": {row["stage"]: round(row["forward_ms"] * 1e3, 2) for row in rows},
+           "stage_frac": {row["stage"]: roofline(row, name)["frac"] for row in rows if row["bound"]}}
+    if len(sequences) > 1:
+        out["seqs_per_s"] = round(len(sequences) / (p50 * 1e-3), 1)
+        out["seqs_per_s_predict"] = round(len(sequences) / (pct(r["api"], 50) * 1e-3), 1)
     if args.cpu_seconds > 0:
-        times, threads, (want, want_acts, _) = cpu_baseline(spec, weights, sequences, questions, args.cpu_seconds)
-        progress(f"cpu baseline: {len(times)} forwards")
-        line["cpu_baseline"] = {
-            "value": round(pct(times, 50), 2), "unit": "ms", "cores": threads, "kind": "port",
-            "sample": f"{len(times)} full forwards of the same 512-token request by the NumPy FP32 oracle "
-                      f"(p50; BLAS threads {threads} of {len(os.sched_getaffinity(0))} host cores)"}
-        worst = max(float(np.abs(r["logits"][q, :len(w)] - w).max()) for q, w in enumerate(want))
-        same = all(int(np.argmax(r["logits"][q, :len(w)])) == int(np.argmax(w)) for q, w in enumerate(want))
-        line["parity"] = {"max_abs_logit_err": worst, "max_abs_act_err": float(np.abs(r["acts"] - want_acts).max()),
-                          "decisions_equal": same}
+        # The oracle on the whole request; for the 64-sequence batch on its first sequence only
+        # (sequences are independent), scaled to the batch.
+        picks = [0] if name == "b64x1024" else list(range(len(sequences)))
+        sub_q = [(picks.index(s), m, k) for s, m, k in questions if s in picks]
+        run = oracle_forward(spec, weights, [sequences[i] for i in picks], sub_q)
+        budget = args.cpu_seconds if name == "l512" else min(args.cpu_seconds, 8.0)
+        times, (want, want_acts, _) = cpu_baseline(run, budget)
+        cpu_ms = pct(times, 50)
+        cores = blas_threads()
+        qrows = [q for q, (s, _, _) in enumerate(questions) if s in picks]
+        if name == "b64x1024":
+            out["cpu_baseline"] = {"value": round(1e3 / cpu_ms, 3), "unit": "seq/s", "cores": cores, "kind": "port",
+                                   "sample": f"{len(times)} oracle FP32 forwards of sequence 0 (1,024 tokens, 24 "
+                                             f"layers; p50 {cpu_ms:.0f} ms) scaled to the 64-sequence batch; BLAS "
+                                             f"threads {cores} of {len(os.sched_getaffinity(0))} host cores"}
+        elif len(sequences) > 1:
+            out["cpu_baseline"] = {"value": round(len(sequences) / (cpu_ms * 1e-3), 3), "unit": "seq/s",
+                                   "cores": cores, "kind": "port",
+                                   "sample": f"{len(times)} oracle FP32 forwards of the whole request (p50 "
+                                             f"{cpu_ms:.0f} ms); BLAS threads {cores} of "
+                                             f"{len(os.sched_getaffinity(0))} host cores"}
+        else:
+            out["cpu_baseline"] = {"value": round(cpu_ms, 3), "unit": "ms", "cores": cores, "kind": "port",
+                                   "sample": f"{len(times)} oracle FP32 forwards of the same request (p50); BLAS "
+                                             f"threads {cores} of {len(os.sched_getaffinity(0))} host cores"}
+        out["parity"] = parity(r["logits"][qrows], r["acts"][qrows], want, want_acts)
+        progress(f"{name}: cpu baseline {len(times)} forwards")
     else:
-        line["cpu_baseline"] = None
-    return line
-
-
-def run_extras(args):
-    from laya_cuda import synthetic
-    from laya_cuda.runtime import Runtime
-
-    extras = {}
-    chosen = args.workloads.split(",") if args.workloads else None
-    for name, dtype in (("l83", "float16"), ("l1024", "float16"), ("ragged32", "float16"),
-                        ("b64x1024", "bfloat16")):
-        if chosen and name not in chosen:
-            continue
-        spec = synthetic.adapter(name, mfma_dtype=dtype)
-        weights = synthetic.weights(spec, seed=0, bf16=synthetic.WORKLOADS[name].get("bf16", False))
-        sequences, questions = synthetic.request(name, seed=1)
-        steps = args.steps if name in ("l83", "l1024") else max(5, args.steps // 20)
-        rt = Runtime(spec, 0, 2, weights=weights)
-        try:
-            r = time_workload(rt, sequences, questions, steps, min(args.warmup, 5), not args.eager)
-            rows = stage_profile(rt, spec, sequences, questions, 3 if name in ("ragged32", "b64x1024") else 20)
-        finally:
-            rt.close()
-        progress(f"{name} timed: p50 {pct(r['gpu'], 50):.4f} ms")
-        flops = synthetic.valid_flops(spec, [len(s) for s in sequences])
-        p50 = pct(r["gpu"], 50)
-        entry = {"p50_ms": round(p50, 4), "p95_ms": round(pct(r["gpu"], 95), 4),
-                 "predict_p50_ms": round(pct(r["api"], 50), 4), "predict_p95_ms": round(pct(r["api"], 95), 4),
-                 "first_ms": round(r["first_ms"], 3), "steps": steps,
-                 "tflops": round(flops / (p50 * 1e-3) / 1e12, 2),
-                 "mfma_frac": round(flops / (p50 * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)}
-        entry["stages_us_per_forward"] = {row["stage"]: round(row["forward_ms"] * 1e3, 2) for row in rows}
-        entry["stage_frac"] = {row["stage"]: round(roofline(row)["frac"], 4) for row in rows if row["bound"]}
-        if len(sequences) > 1:
-            entry["seqs_per_s"] = round(len(sequences) / (p50 * 1e-3), 1)
-            entry["seqs_per_s_predict"] = round(len(sequences) / (pct(r["api"], 50) * 1e-3), 1)
-        extras[name] = entry
-        del weights
-    return extras
-
-
-def _drive(submit, work, concurrency, samples, warmup):
-    """Keep ``concurrency`` requests outstanding until ``samples`` complete; per-request latency is
-    taken at completion (a done-callback), not when the driver polls (tools/benchmark_batching.py
-    protocol of the reference)."""
-    from concurrent.futures import FIRST_COMPLETED, Future, wait
-    for i in range(0, warmup, concurrency):
-        for f in [submit(*work[j % len(work)]) for j in range(i, min(i + concurrency, warmup))]:
-            f.result()
-    pending, latencies, sent = {}, [], 0
-    start = time.perf_counter()
-    while sent < samples or pending:
-        while sent < samples and len(pending) < concurrency:
-            before = time.perf_counter()
-            original, done = submit(*work[sent % len(work)]), Future()
-
-            def complete(f, finished=done):
-                try:
-                    f.result()
-                    finished.set_result(time.perf_counter())
-                except BaseException as error:  # reported by the driver
-                    finished.set_exception(error)
-            original.add_done_callback(complete)
-            pending[done] = before
-            sent += 1
-        finished, _ = wait(pending, return_when=FIRST_COMPLETED)
-        for f in finished:
-            latencies.append((f.result() - pending.pop(f)) * 1e3)
-    seconds = time.perf_counter() - start
-    return {"p50_ms": round(pct(latencies, 50), 3), "p95_ms": round(pct(latencies, 95), 3),
-            "p99_ms": round(pct(latencies, 99), 3), "requests_s": round(samples / seconds, 1)}
-
-
-def run_batching(args):
-    """Serialized Engine vs BatchEngine under bounded outstanding load on the 12-layer d=768 encoder
-    (tools/benchmark_batching.py of the reference): one 2-option question per request, short
-    (32-token), long (1,024-token) and alternating cases, 1 / 8 / 32 requests outstanding."""
-    import shutil
-    import tempfile
-    from concurrent.futures import ThreadPoolExecutor
-
-    from laya_cuda import BatchEngine, Engine, synthetic
-    spec = synthetic.WORKLOADS["ragged32"]
-    config = synthetic.encoder_config(spec["layers"], spec["width"], spec["heads"], spec["intermediate"],
-                                      spec["vocab"], spec["positions"])
-    task = dict(synthetic.task_config(spec["max_len"]), head_max_len=64)
-    root = tempfile.mkdtemp(prefix="laya_batching_")
-    out = {"model": "12L/768 post-LN encoder, fp16 operands, max_len 1024", "samples": args.batching_samples,
-           "batch_tokens": 4096, "cases": {}}
-    try:
-        path = synthetic.checkpoint(root, config, task, seed=0, random_norms=False)[0]
-        questions = {"0": {"type": "choice", "instructions": "Choose a topic.", "criteria": ["payment", "software"]}}
-        probe = Engine(str(path), max_cached_shapes=2)
-        overhead = len(probe.adapter.prepare("", questions)[0][0])
-        probe.close()
-        short = (" refund" * max(0, 32 - overhead), questions)
-        long = (" refund" * max(0, spec["max_len"] - overhead), questions)
-        cases = {"short": [short], "long": [long], "mixed": [short, long]}
-        for mode in ("serial", "batch"):
-            executor = ThreadPoolExecutor(1) if mode == "serial" else None
-            engine = (executor.submit(Engine, str(path)).result() if executor
-                      else BatchEngine(str(path), max_batch_tokens=4096))
-            submit = ((lambda st, q: executor.submit(engine.predict, st, q)) if executor else engine.submit)
-            try:
-                for case, work in cases.items():
-                    for concurrency in (1, 8, 32):
-                        r = _drive(submit, work, concurrency, args.batching_samples, 20)
-                        out["cases"].setdefault(case, {}).setdefault(mode, {})[str(concurrency)] = r
-                        progress(f"batching {case} {mode} x{concurrency}: p50 {r['p50_ms']} ms, {r['requests_s']} req/s")
-            finally:
-                if executor:
-                    executor.submit(engine.close).result()
-                    executor.shutdown()
-                else:
-                    engine.close()
-    finally:
-        shutil.rmtree(root, ignore_errors=True)
+        out["cpu_baseline"] = None
     return out
 
 
-def _sync():
+def synthetic_checkpoint(root, layers=12, width=768, heads=12, intermediate=3072, vocab=50368, max_len=512):
+    from laya_cuda import synthetic
+    config = synthetic.encoder_config(layers, width, heads, intermediate, vocab, max_len)
+    task = dict(synthetic.task_config(max_len), head_max_len=64)
+    return synthetic.checkpoint(root, config, task, seed=0, random_norms=False)[0]
+
+
+QUESTION = {"0": {"type": "choice", "instructions": "Choose a team for billing questions.",
+                  "criteria": ["payment", "software", "delivery", "other"]}}
+
+
+def run_engine_predict(path, args):
+    """Engine.predict at 512 tokens: the request is tokenised, packed, run and decoded on every call
+    (the reference measures predict this way, including tokenisation and decode)."""
+    from laya_cuda import Engine
+    with Engine(str(path), max_cached_shapes=4) as engine:
+        state = "the customer asks about a late delivery and wants a refund " * 80
+        items = engine.adapter.prepare(state, QUESTION)
+        tokens = [len(i[0]) for i in items]
+        for _ in range(args.warmup + 1):
+            engine.predict(state, QUESTION)
+        api, gpu = [], []
+        for _ in range(args.steps):
+            s = time.perf_counter()
+            engine.predict(state, QUESTION)
+            api.append((time.perf_counter() - s) * 1e3)
+            gpu.append(engine.last_metrics["gpu_ms"])
+        prep = []
+        for _ in range(args.steps):
+            s = time.perf_counter()
+            engine.adapter.prepare(state, QUESTION)
+            prep.append((time.perf_counter() - s) * 1e3)
+    return {"model": "12L/768 post-LN encoder, fp16 operands, synthetic checkpoint with a BPE tokenizer trained "
+                     "offline; one 4-option choice question", "tokens_per_question": tokens, "steps": args.steps,
+            "p50_ms": round(pct(api, 50), 4), "p95_ms": round(pct(api, 95), 4),
+            "gpu_p50_ms": round(pct(gpu, 50), 4), "prepare_p50_ms": round(pct(prep, 50), 4)}
+
+
+def closed_loop(call, requests, clients, per_client):
+    """`clients` threads, each issuing `per_client` requests one after another (a request waits
+    for the previous answer of its thread): per-request latency percentiles and requests/s."""
+    latencies, errors = [], []
+    lock = threading.Lock()
+
+    def client(c):
+        mine = []
+        for i in range(per_client):
+            state, questions = requests[(c + i) % len(requests)]
+            s = time.perf_counter()
+            try:
+                call(state, questions)
+            except Exception as error:  # reported, not raised, so the run finishes
+                errors.append(repr(error))
+            mine.append((time.perf_counter() - s) * 1e3)
+        with lock:
+            latencies.extend(mine)
+
+    threads = [threading.Thread(target=client, args=(c,)) for c in range(clients)]
+    start = time.perf_counter()
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    seconds = time.perf_counter() - start
+    return {"p50_ms": round(pct(latencies, 50), 3), "p95_ms": round(pct(latencies, 95), 3),
+            "p99_ms": round(pct(latencies, 99), 3), "requests_s": round(len(latencies) / seconds, 1),
+            "requests": len(latencies), "errors": errors[:3]}
+
+
+def run_batching(path, args):
+    """A serialised Engine (one lock, as a single-owner service would hold it) against BatchEngine,
+    with 1, 8 and 32 closed-loop clients on short (32-token), long (512-token) and alternating
+    requests.  BatchEngine keeps at most 4 shape slots, so the mixed case also reports how often a
+    pack needed a new slot (graph capture) under that LRU bound."""
+    from laya_cuda import BatchEngine, Engine
+    probe = Engine(str(path), max_cached_shapes=1)
+    overhead = len(probe.adapter.prepare("", QUESTION)[0][0])
+    probe.close()
+    short = (" refund" * max(1, 32 - overhead), QUESTION)
+    long = ("the customer asks about a late delivery and wants a refund " * 80, QUESTION)
+    cases = {"short": [short], "long": [long], "mixed": [short, long]}
+    per = max(8, args.batching_requests)
+    out = {"requests_per_client": per, "max_batch_tokens": 8192, "max_cached_shapes": 4, "cases": {}}
+    engine = Engine(str(path), max_cached_shapes=4)
+    guard = threading.Lock()
+
+    def serial(state, questions):
+        with guard:
+            return engine.predict(state, questions)
     try:
-        import torch
-        if torch.cuda.is_available():
-            torch.cuda.synchronize()
-    except ImportError:
-        pass
+        for case, work in cases.items():
+            for clients in (1, 8, 32):
+                serial(*work[0])
+                r = closed_loop(serial, work, clients, per if clients < 32 else max(4, per // 2))
+                out["cases"].setdefault(case, {}).setdefault("serial", {})[str(clients)] = r
+    finally:
+        engine.close()
+    misses = {"packs": 0, "cache_miss": 0}
+    with BatchEngine(str(path), max_batch_size=16, max_batch_tokens=8192, max_wait_ms=1,
+                     max_cached_shapes=4) as batch:
+        def batched(state, questions):
+            future = batch.submit(state, questions)
+            result = future.result(120)
+            with guard:
+                misses["packs"] += 1
+                misses["cache_miss"] += bool(future.metrics.get("cache_miss"))
+            return result
+        for case, work in cases.items():
+            for clients in (1, 8, 32):
+                batched(*work[0])
+                r = closed_loop(batched, work, clients, per if clients < 32 else max(4, per // 2))
+                out["cases"].setdefault(case, {}).setdefault("batch", {})[str(clients)] = r
+                progress(f"batching {case} x{clients}: batch p50 {r['p50_ms']} ms {r['requests_s']} req/s, serial "
+                         f"{out['cases'][case]['serial'][str(clients)]['requests_s']} req/s")
+    out["batch_requests_with_new_slot"] = misses
+    return out
 
 
 def main():
@@ -346,26 +380,55 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--stage-reps", type=int, default=50)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--extras", action="store_true")
-    ap.add_argument("--eager", action="store_true")
-    ap.add_argument("--calibrate-copy", action="store_true")
-    ap.add_argument("--batching", action="store_true",
-                    help="with --extras: serialized Engine vs BatchEngine under 1/8/32 outstanding requests")
-    ap.add_argument("--batching-samples", type=int, default=100)
-    ap.add_argument("--workloads", default="",
-                    help="with --extras: comma-separated subset of l83,l1024,ragged32,b64x1024 (default all)")
+    ap.add_argument("--stage-reps", type=int, default=10, help="eager forwards per stage for the stage timings")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="oracle time budget of the headline (0: none)")
+    ap.add_argument("--only", default="", help="comma-separated subset of " + ",".join(
+        list(WORKLOADS) + ["engine", "batching"]) + " (default all; l512 is always the headline)")
+    ap.add_argument("--batching-requests", type=int, default=24, help="requests per closed-loop client")
+    ap.add_argument("--eager", action="store_true", help="launch kernel by kernel instead of replaying hipGraphs")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run a 64 MiB device copy (the reference size for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the encoder path shards by request with no collective, and "
               "multi-GPU runs are not part of this build (use --gpus 1)", file=sys.stderr)
         sys.exit(2)
-    line = run_headline(args)
-    if args.extras:
-        line["extras"] = run_extras(args)
-        if args.batching:
-            line["extras"]["batching"] = run_batching(args)
+    chosen = set(args.only.split(",")) if args.only else set(WORKLOADS) | {"engine", "batching"}
+    if args.calibrate_copy:
+        import torch
+        src = torch.ones(16 << 20, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        progress("copy calibration done")
+
+    head = run_workload("l512", args)
+    line = {"metric": METRIC, "value": head["p50_ms"], "unit": "ms", "n_gpus": 1, "steps": head["steps"],
+            "warmup": head["warmup"], "ms_per_step": head["ms_per_step"], "higher_is_better": False,
+            "scaling": "weak", "vs_baseline": None, "dtype": head["dtype"], "data": "synthetic",
+            "config": {"workload": "l512: " + head["workload"], "seq_len": 512, "global_batch": 1,
+                       "parallelism": "single GPU"}}
+    for key in ("p95_ms", "predict_p50_ms", "predict_p95_ms", "first_ms", "graph_replay", "tflops_forward",
+                "roofline", "stages_us_per_forward", "cpu_baseline", "parity"):
+        if key in head:
+            line[key] = head[key]
+    line["workloads"] = {}
+    for name in ("l83", "l1024", "ragged32", "b64x1024"):
+        if name in chosen:
+            line["workloads"][name] = run_workload(name, args)
+    if chosen & {"engine", "batching"}:
+        root = tempfile.mkdtemp(prefix="laya_bench_")
+        try:
+            path = synthetic_checkpoint(root)
+            if "engine" in chosen:
+                line["engine_predict_l512"] = run_engine_predict(path, args)
+                progress(f"engine predict p50 {line['engine_predict_l512']['p50_ms']} ms")
+            if "batching" in chosen:
+                line["batching"] = run_batching(path, args)
+        finally:
+            shutil.rmtree(root, ignore_errors=True)
     print(json.dumps(line), flush=True)
 
 

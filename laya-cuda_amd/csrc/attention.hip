@@ -438,18 +438,18 @@ hipError_t launch_t(const AttnArgs& a, int mode, int waves, hipStream_t stream) 
   const dim3 grid(a.max_tiles, a.heads);
   if (mode == kAttnSplitKeys) {
     switch (waves) {
-      case 2: hipLaunchKernelGGL((attention_split_kernel<T, 2>), grid, dim3(128), 0, stream, a); break;
-      case 4: hipLaunchKernelGGL((attention_split_kernel<T, 4>), grid, dim3(256), 0, stream, a); break;
-      case 8: hipLaunchKernelGGL((attention_split_kernel<T, 8>), grid, dim3(512), 0, stream, a); break;
+      case 2: LAYA_LAUNCH((attention_split_kernel<T, 2>), grid, dim3(128), 0, stream, a); break;
+      case 4: LAYA_LAUNCH((attention_split_kernel<T, 4>), grid, dim3(256), 0, stream, a); break;
+      case 8: LAYA_LAUNCH((attention_split_kernel<T, 8>), grid, dim3(512), 0, stream, a); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
   }
   switch (waves) {
-    case 1: hipLaunchKernelGGL((attention_kernel<T, 1>), grid, dim3(64), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((attention_kernel<T, 2>), grid, dim3(128), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((attention_kernel<T, 4>), grid, dim3(256), 0, stream, a); break;
-    case 8: hipLaunchKernelGGL((attention_kernel8<T>), grid, dim3(512), 0, stream, a); break;
+    case 1: LAYA_LAUNCH((attention_kernel<T, 1>), grid, dim3(64), 0, stream, a); break;
+    case 2: LAYA_LAUNCH((attention_kernel<T, 2>), grid, dim3(128), 0, stream, a); break;
+    case 4: LAYA_LAUNCH((attention_kernel<T, 4>), grid, dim3(256), 0, stream, a); break;
+    case 8: LAYA_LAUNCH((attention_kernel8<T>), grid, dim3(512), 0, stream, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -1,12 +1,33 @@
 // Shared device helpers for the gfx950 (CDNA4) encoder kernels.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include <cstddef>
 
 namespace laya {
+
+// Kernel-level timing on request: when the host has set `launch_timing` on this thread, the next
+// LAYA_LAUNCH records that event pair from the kernel's own dispatch (hipExtLaunchKernel: start
+// and end of the kernel, the interval a kernel trace reports, without the extra stream packets of
+// hipEventRecord around the launch) and clears it.  Never set while a stream is being captured.
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+inline thread_local LaunchTiming launch_timing;
+
+#define LAYA_LAUNCH(kernel, grid, block, lds, stream, ...)                                          \
+  do {                                                                                              \
+    if (::laya::launch_timing.start) {                                                              \
+      hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, ::laya::launch_timing.start,          \
+                            ::laya::launch_timing.stop, 0, __VA_ARGS__);                            \
+      ::laya::launch_timing = ::laya::LaunchTiming{};                                              \
+    } else {                                                                                        \
+      hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                            \
+    }                                                                                               \
+  } while (0)
 
 // 16-bit MFMA operand types.  Storage in HBM is raw 16-bit; arithmetic is always fp32.
 typedef __bf16 bf16;

@@ -761,11 +761,11 @@ hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
   const size_t lds = lds_bytes(d);
   switch (tile) {
 #define LAYA_TILE(ID, BM_, BN_, WM_, WN_, PF_) \
-  case ID: hipLaunchKernelGGL((gemm_kernel<T, BM_, BN_, WM_, WN_, PF_, E>), grid, block, lds, stream, a); break;
+  case ID: LAYA_LAUNCH((gemm_kernel<T, BM_, BN_, WM_, WN_, PF_, E>), grid, block, lds, stream, a); break;
 #define LAYA_PIPE(ID, BM_, BN_, WM_, WN_, BK_, ST_) \
-  case ID: hipLaunchKernelGGL((gemm_pipe_kernel<T, BM_, BN_, WM_, WN_, BK_, ST_, E, false>), grid, block, lds, stream, a); break;
+  case ID: LAYA_LAUNCH((gemm_pipe_kernel<T, BM_, BN_, WM_, WN_, BK_, ST_, E, false>), grid, block, lds, stream, a); break;
 #define LAYA_RING(ID, BM_, BN_, WM_, WN_) \
-  case ID: hipLaunchKernelGGL((gemm_pipe_kernel<T, BM_, BN_, WM_, WN_, 64, 5, E, true>), grid, block, lds, stream, a); break;
+  case ID: LAYA_LAUNCH((gemm_pipe_kernel<T, BM_, BN_, WM_, WN_, 64, 5, E, true>), grid, block, lds, stream, a); break;
     LAYA_PIPE(0, 256, 256, 2, 2, 64, 2)
     LAYA_PIPE(1, 256, 128, 2, 2, 64, 2)
     LAYA_TILE(2, 128, 128, 2, 2, 2)

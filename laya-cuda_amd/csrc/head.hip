@@ -255,7 +255,7 @@ hipError_t launch_head_gather(const HeadGatherArgs& a, int width, hipStream_t st
   if (a.cap <= 0) return hipSuccess;
   const dim3 grid((a.cap + 3) / 4), block(256);
   switch (width) {
-#define LAYA_CASE(D) case D: hipLaunchKernelGGL((head_gather_kernel<D>), grid, block, 0, stream, a); break;
+#define LAYA_CASE(D) case D: LAYA_LAUNCH((head_gather_kernel<D>), grid, block, 0, stream, a); break;
     LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
     LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
 #undef LAYA_CASE
@@ -271,8 +271,8 @@ hipError_t launch_gather_rows(const GatherRowsArgs& a, int width, DType t, hipSt
   switch (width) {
 #define LAYA_CASE(D)                                                                                      \
   case D:                                                                                               \
-    if (h) hipLaunchKernelGGL((gather_rows_kernel<D, f16>), grid, block, 0, stream, a);                  \
-    else hipLaunchKernelGGL((gather_rows_kernel<D, bf16>), grid, block, 0, stream, a);                   \
+    if (h) LAYA_LAUNCH((gather_rows_kernel<D, f16>), grid, block, 0, stream, a);                  \
+    else LAYA_LAUNCH((gather_rows_kernel<D, bf16>), grid, block, 0, stream, a);                   \
     break;
     LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
     LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
@@ -293,7 +293,7 @@ hipError_t launch_head_gemm(const HeadGemmArgs& a, hipStream_t stream) {
   if (a.cap <= 0) return hipSuccess;
   if (a.N % 64 || a.K % (a.splits * 32)) return hipErrorInvalidValue;
   const dim3 grid(a.N / 64, (a.cap + 31) / 32, a.splits);
-  hipLaunchKernelGGL(head_gemm_kernel, grid, dim3(256), 0, stream, a);
+  LAYA_LAUNCH(head_gemm_kernel, grid, dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -301,7 +301,7 @@ hipError_t launch_head_logit(const HeadLogitArgs& a, int width, hipStream_t stre
   if (a.cap <= 0) return hipSuccess;
   const dim3 grid((a.cap + 3) / 4), block(256);
   switch (width) {
-#define LAYA_CASE(D) case D: hipLaunchKernelGGL((head_logit_kernel<D>), grid, block, 0, stream, a); break;
+#define LAYA_CASE(D) case D: LAYA_LAUNCH((head_logit_kernel<D>), grid, block, 0, stream, a); break;
     LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
     LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
 #undef LAYA_CASE
@@ -313,7 +313,7 @@ hipError_t launch_head_logit(const HeadLogitArgs& a, int width, hipStream_t stre
 hipError_t launch_head_features(const HeadFeatureArgs& a, hipStream_t stream) {
   if (a.b <= 0) return hipSuccess;
   if (a.kp < a.width + 4) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(head_features_kernel, dim3(a.b), dim3(256), 0, stream, a);
+  LAYA_LAUNCH(head_features_kernel, dim3(a.b), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -321,7 +321,7 @@ hipError_t launch_act_out(const ActOutArgs& a, hipStream_t stream) {
   if (a.b <= 0) return hipSuccess;
   const size_t lds = static_cast<size_t>(a.hidden) * sizeof(float);
   if (lds > 64 * 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(act_out_kernel, dim3(a.b), dim3(256), lds, stream, a);
+  LAYA_LAUNCH(act_out_kernel, dim3(a.b), dim3(256), lds, stream, a);
   return hipGetLastError();
 }
 

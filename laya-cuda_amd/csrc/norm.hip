@@ -116,7 +116,7 @@ template <typename T>
 hipError_t launch_embed_t(const EmbedArgs& a, int width, hipStream_t stream) {
   const dim3 grid((a.rows + 3) / 4), block(256);
   switch (width) {
-#define LAYA_CASE(D) case D: hipLaunchKernelGGL((embed_norm_kernel<D, T>), grid, block, 0, stream, a); break;
+#define LAYA_CASE(D) case D: LAYA_LAUNCH((embed_norm_kernel<D, T>), grid, block, 0, stream, a); break;
     LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
     LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
 #undef LAYA_CASE
@@ -129,10 +129,10 @@ template <typename T, int D>
 void launch_add_norm_d(const AddNormArgs& a, dim3 grid, dim3 block, hipStream_t stream) {
   const int ns = !a.parts ? 0 : a.splits <= kMaxFixedSplits ? a.splits : -1;
   switch (ns) {
-#define LAYA_NS(N) case N: hipLaunchKernelGGL((add_norm_kernel<D, T, N>), grid, block, 0, stream, a); break;
+#define LAYA_NS(N) case N: LAYA_LAUNCH((add_norm_kernel<D, T, N>), grid, block, 0, stream, a); break;
     LAYA_NS(0) LAYA_NS(1) LAYA_NS(2) LAYA_NS(3) LAYA_NS(4) LAYA_NS(5) LAYA_NS(6) LAYA_NS(7) LAYA_NS(8)
 #undef LAYA_NS
-    default: hipLaunchKernelGGL((add_norm_kernel<D, T, -1>), grid, block, 0, stream, a); break;
+    default: LAYA_LAUNCH((add_norm_kernel<D, T, -1>), grid, block, 0, stream, a); break;
   }
 }
 

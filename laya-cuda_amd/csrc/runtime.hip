@@ -749,19 +749,35 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
   }
 }
 
-void forward(Engine& E, Slot& s) {
-  launch_stage(E, s, kEmbed, 0);
+// The whole forward on the engine's stream.  With `marks`, the kernel of every launch of stage
+// `marked` records marks[2i] and marks[2i+1] at its start and end (its i-th launch), for timing
+// the stage where it runs in the forward.
+void forward(Engine& E, Slot& s, int marked = -1, hipEvent_t* marks = nullptr) {
+  int mark = 0;
+  auto run = [&](int stage, int layer) {
+    const bool timed = marks && stage == marked;
+    if (timed) {
+      launch_timing = LaunchTiming{marks[2 * mark], marks[2 * mark + 1]};
+      ++mark;
+    }
+    launch_stage(E, s, stage, layer);
+    if (timed && launch_timing.start) {  // the stage launched nothing (no rows): nothing to time
+      launch_timing = LaunchTiming{};
+      throw Failure{LAYA_EINVAL, "timed stage launched no kernel"};
+    }
+  };
+  run(kEmbed, 0);
   for (int i = 0; i < E.cfg.layers; ++i)
-    for (int stage = kQkv; stage <= kFfnNorm; ++stage) launch_stage(E, s, stage, i);
+    for (int stage = kQkv; stage <= kFfnNorm; ++stage) run(stage, i);
   if (E.modern) {
-    launch_stage(E, s, kTypeNorm, 0);
+    run(kTypeNorm, 0);
     for (int j = 0; j < E.cfg.head_layers; ++j)
       for (int stage = kHlQkv; stage <= kHlNorm; ++stage)
-        if (stage_used(E, stage, j)) launch_stage(E, s, stage, j);
+        if (stage_used(E, stage, j)) run(stage, j);
   } else {
-    launch_stage(E, s, kHeadGather, 0);
+    run(kHeadGather, 0);
   }
-  for (int stage = kHeadScorer; stage < kStageCount; ++stage) launch_stage(E, s, stage, 0);
+  for (int stage = kHeadScorer; stage < kStageCount; ++stage) run(stage, 0);
 }
 
 // ModernBERT variant: layer tables and the RoPE cos/sin tables of both thetas (runtime.py:159-165:
@@ -1222,6 +1238,36 @@ int laya_time_stage(void* handle, const int32_t* host_packed, const LayaShape* s
   return guarded(E, [&] {
     LAYA_REQUIRE(avg_ms && reps >= 1 && reps <= 100000, "reps must be in [1, 100000]");
     LAYA_REQUIRE(stage >= 0 && stage < kStageCount, "unknown stage");
+    if (layer == -1) {  // in-forward timing: every kernel of the stage inside `reps` eager forwards
+      int launches = 0;
+      const int span = per_layer(stage) ? E->cfg.layers : per_head_layer(stage) ? E->cfg.head_layers : 1;
+      for (int j = 0; j < span; ++j) launches += stage_used(*E, stage, j);
+      LAYA_REQUIRE(launches > 0, "stage not in this model's forward");
+      bool miss = false;
+      Slot* s = stage_inputs(E, host_packed, shape, &miss);
+      std::vector<hipEvent_t> marks(2 * static_cast<size_t>(launches), nullptr);
+      double total = 0.0;
+      try {
+        for (hipEvent_t& e : marks) LAYA_HIP(hipEventCreate(&e));
+        forward(*E, *s);  // warm: the first forward of a fresh slot pays first-touch costs
+        for (int r = 0; r < reps; ++r) {
+          forward(*E, *s, stage, marks.data());
+          LAYA_HIP(hipStreamSynchronize(E->stream));
+          for (int i = 0; i < launches; ++i) {
+            float ms = 0.f;
+            LAYA_HIP(hipEventElapsedTime(&ms, marks[2 * i], marks[2 * i + 1]));
+            total += ms;
+          }
+        }
+      } catch (...) {
+        for (hipEvent_t e : marks)
+          if (e) (void)hipEventDestroy(e);
+        throw;
+      }
+      for (hipEvent_t e : marks) (void)hipEventDestroy(e);
+      *avg_ms = static_cast<float>(total / (static_cast<double>(reps) * launches));
+      return;
+    }
     LAYA_REQUIRE(stage_used(*E, stage, layer), "stage or layer not in this model's forward");
     bool miss = false;
     Slot* s = stage_inputs(E, host_packed, shape, &miss);
