@@ -94,6 +94,24 @@ typedef struct LayaMetrics {
  */
 int64_t laya_packed_ints(const LayaShape* shape);
 
+/* One HIP device as the doctor reports it (laya_cuda/cli.py:118-176 reports CUDA devices through
+ * CuPy; here the library itself answers, from hipGetDeviceProperties and hipMemGetInfo). */
+typedef struct LayaDevice {
+  char name[256];
+  char arch[64];            /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int64_t hbm_bytes;        /* total device memory */
+  int64_t free_bytes;       /* free device memory now */
+  int32_t compute_units;
+  int32_t lds_bytes_per_cu;
+  int32_t clock_khz;
+  int32_t supported;        /* 1: gfx950, the architecture this library is built for */
+} LayaDevice;
+
+/* Number of HIP devices (0 without a driver or device: not an error). */
+int laya_device_count(int* count);
+/* Properties of HIP device `device`. */
+int laya_device_info(int device, LayaDevice* out);
+
 /* Runtime(adapter, device, max_cached_shapes) construction (runtime.py:137-146). */
 int laya_create(const LayaConfig* cfg, int device, int max_slots, void** handle);
 

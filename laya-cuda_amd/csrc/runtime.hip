@@ -921,6 +921,51 @@ int64_t laya_packed_ints(const LayaShape* shape) {
   return static_cast<int64_t>(make_layout(shape->rows, shape->batch, shape->options).user_end);
 }
 
+int laya_device_count(int* count) {
+  return guarded(nullptr, [&] {
+    LAYA_REQUIRE(count != nullptr, "null argument");
+    int n = 0;
+    const hipError_t e = hipGetDeviceCount(&n);
+    if (e == hipErrorNoDevice || e == hipErrorInsufficientDriver) {
+      (void)hipGetLastError();
+      n = 0;
+    } else {
+      LAYA_HIP(e);
+    }
+    *count = n;
+  });
+}
+
+int laya_device_info(int device, LayaDevice* out) {
+  return guarded(nullptr, [&] {
+    LAYA_REQUIRE(out != nullptr, "null argument");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    LAYA_REQUIRE(device >= 0 && device < n, "no HIP device " + std::to_string(device));
+    hipDeviceProp_t p;
+    LAYA_HIP(hipGetDeviceProperties(&p, device));
+    std::memset(out, 0, sizeof(*out));
+    std::strncpy(out->name, p.name, sizeof(out->name) - 1);
+    std::strncpy(out->arch, p.gcnArchName, sizeof(out->arch) - 1);
+    out->hbm_bytes = static_cast<int64_t>(p.totalGlobalMem);
+    out->compute_units = p.multiProcessorCount;
+    out->lds_bytes_per_cu = static_cast<int32_t>(p.maxSharedMemoryPerMultiProcessor);
+    out->clock_khz = p.clockRate;
+    out->supported = std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
+    int current = 0;
+    LAYA_HIP(hipGetDevice(&current));
+    LAYA_HIP(hipSetDevice(device));
+    size_t free_bytes = 0, total = 0;
+    const hipError_t e = hipMemGetInfo(&free_bytes, &total);
+    (void)hipSetDevice(current);
+    LAYA_HIP(e);
+    out->free_bytes = static_cast<int64_t>(free_bytes);
+  });
+}
+
 int laya_create(const LayaConfig* cfg, int device, int max_slots, void** handle) {
   if (!handle || !cfg) return fail(nullptr, Failure{LAYA_EINVAL, "null argument"});
   *handle = nullptr;

@@ -32,6 +32,12 @@ class LayaMetrics(ct.Structure):
                 ("graph_replay", ct.c_int32), ("owned_gpu_bytes", ct.c_int64)]
 
 
+class LayaDevice(ct.Structure):
+    _fields_ = [("name", ct.c_char * 256), ("arch", ct.c_char * 64), ("hbm_bytes", ct.c_int64),
+                ("free_bytes", ct.c_int64), ("compute_units", ct.c_int32), ("lds_bytes_per_cu", ct.c_int32),
+                ("clock_khz", ct.c_int32), ("supported", ct.c_int32)]
+
+
 _p, _i, _f, _i64 = ct.c_void_p, ct.c_int, ct.c_float, ct.c_int64
 _ip = ct.POINTER(ct.c_int32)
 _fp = ct.POINTER(ct.c_float)
@@ -39,6 +45,8 @@ _fp = ct.POINTER(ct.c_float)
 SIGNATURES = {
     "laya_abi_version": ([], _i),
     "laya_packed_ints": ([ct.POINTER(LayaShape)], _i64),
+    "laya_device_count": ([ct.POINTER(ct.c_int)], _i),
+    "laya_device_info": ([_i, ct.POINTER(LayaDevice)], _i),
     "laya_create": ([ct.POINTER(LayaConfig), _i, _i, ct.POINTER(_p)], _i),
     "laya_load_weight": ([_p, ct.c_char_p, _p, _i, ct.POINTER(_i64), _i], _i),
     "laya_finalize": ([_p], _i),

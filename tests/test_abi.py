@@ -143,6 +143,20 @@ def test_create_rejects_unbuilt_variants_before_touching_the_device():
     assert "64-wide" in _lib.error(None)
 
 
+def test_device_queries():
+    """laya_device_count reports zero devices (not an error) without a GPU; laya_device_info
+    refuses a device that does not exist."""
+    lib = _lib.load()
+    count = ct.c_int(-1)
+    assert lib.laya_device_count(ct.byref(count)) == _lib.OK and count.value >= 0
+    info = _lib.LayaDevice()
+    assert lib.laya_device_info(count.value, ct.byref(info)) != _lib.OK
+    assert "no HIP device" in _lib.error(None)
+    if count.value:
+        assert lib.laya_device_info(0, ct.byref(info)) == _lib.OK
+        assert info.hbm_bytes > 0 and info.compute_units > 0 and info.free_bytes <= info.hbm_bytes
+
+
 def test_stage_queries_without_a_handle():
     lib = _lib.load()
     names = [lib.laya_stage_name(i).decode() for i in range(lib.laya_stage_count())]
