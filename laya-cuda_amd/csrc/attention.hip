@@ -19,6 +19,8 @@
 //     V^T's LDS rows store keys permuted within each 16-key group to match that lane order.
 #include "kernels.hpp"
 
+#include <algorithm>
+
 namespace laya {
 
 namespace {
@@ -486,6 +488,16 @@ int build_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_s
     if (!run(st, 0, -1) || !run(e, st, len)) return -1;
   }
   if (!run(m, 0, -1)) return -1;
+  // Longest key ranges first: workgroups start in list order, so the long tiles of a ragged batch
+  // do not end up in the last round (their cost grows with the key count).  Ties by first row: a
+  // total order, so the list is the same on every call (std::sort allocates nothing).
+  struct Quad {
+    int32_t v[4];
+  };
+  Quad* quads = reinterpret_cast<Quad*>(tiles);
+  std::sort(quads, quads + nt, [](const Quad& x, const Quad& y) {
+    return x.v[3] != y.v[3] ? x.v[3] > y.v[3] : x.v[0] < y.v[0];
+  });
   for (int t = nt; t < max_tiles; ++t) {
     tiles[4 * t] = tiles[4 * t + 1] = tiles[4 * t + 2] = 0;
     tiles[4 * t + 3] = -1;

@@ -844,9 +844,10 @@ hipError_t gemm_prepare() {
   return e;
 }
 
-// Measured plans: for the batch-1 GEMM problems of the encoder shapes in gemm_plans.inc (written by
-// tune_gemm_plans.py on an MI355X), the (tile, split-K) launch that timed fastest where it beat the
-// heuristic below by more than 3%.  Keyed by CU count, so another part keeps the heuristic.
+// Measured plans: for the batch-1 GEMM problems of the encoder shapes in gemm_plans.inc (each timed
+// on an MI355X through the op-level entry points with every tile and split count), the (tile,
+// split-K) launch that timed fastest where it beat the heuristic below by more than 3%.  Keyed by
+// CU count, so another part keeps the heuristic.
 struct PlanEntry {
   int cus, M, N, K, epi, dtype, rope, tile, splits;
 };

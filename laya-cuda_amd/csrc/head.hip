@@ -76,6 +76,10 @@ __global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
   const int n_rows = *a.n_rows;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, z = blockIdx.z;
   if (m0 >= a.cap) return;
+  // Row blocks past the live rows exit at once (ragged batches fill a small part of their
+  // capacity); the first row block never waits for the count, so batch-1 launches keep their
+  // operand loads ahead of it.
+  if (m0 > 0 && m0 >= n_rows) return;
   __shared__ __align__(16) float sA[BM][KP];
   __shared__ __align__(16) float sB[BN][KP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
