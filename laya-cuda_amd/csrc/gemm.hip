@@ -877,6 +877,29 @@ void gemm_plan(int M, int N, int K, Epi epi, DType t, int cus, int* tile, int* s
   // RoPE-capable tile is 128 or more columns wide.
   const int order[] = {19, 9, 8, 20, 1, 18, 15, 16, 14, 17};
   int best = rope ? (N % 128 ? 10 : 16) : 14, best_split = 1;
+  if (M >= kBatchedRows) {
+    // Batched problems: the main loops are bound by each CU's operand stream from L2, so a launch
+    // takes about (tiles per CU, rounded up) x (BM + BN) x K operand bytes per CU.  That favours
+    // the 256x256 ring even when it leaves CUs idle: on a 15,360 x 768 x 3,072 problem its 180
+    // tiles (one round) beat the 360 tiles of 128x256 (two rounds of 1.5x the bytes per FLOP).
+    long long best_cost = -1;
+    for (int id : {19, 9, 8, 1, 18}) {
+      const TileDef& d = kTiles[id];
+      if (N % d.bn || (rope && (d.bn / d.wn) % 64)) continue;
+      const long long rows = (M + d.bm - 1) / d.bm;
+      if ((rows * d.bm - M) * 4 > M) continue;  // more than 25% padding rows
+      const long long cost = (rows * (N / d.bn) + cus - 1) / cus * (d.bm + d.bn);
+      if (best_cost < 0 || cost < best_cost) {
+        best = id;
+        best_cost = cost;
+      }
+    }
+    if (best_cost >= 0) {
+      *tile = best;
+      *splits = 1;
+      return;
+    }
+  }
   for (int id : order) {
     const TileDef& d = kTiles[id];
     if (N % d.bn) continue;

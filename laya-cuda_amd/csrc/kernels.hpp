@@ -75,6 +75,9 @@ struct GemmTile {
 };
 int gemm_tile_count();
 GemmTile gemm_tile(int id);
+// Packed rows from which a problem counts as batched: the planner costs tiles by their operand
+// bytes per CU, and shape slots keep the out/down projections as 16-bit rows (no split-K).
+constexpr int kBatchedRows = 4096;
 // Chooses a tile and split count for a problem on `cus` compute units: the measured plan table
 // (gemm_plans.inc) when it has the problem and `measured`, else the heuristic.
 // rope: the QKV epilogue applies RoPE, which needs wave tiles of 64-column multiples.

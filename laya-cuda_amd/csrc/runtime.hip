@@ -343,7 +343,7 @@ void destroy_slot(Engine& E, Slot* s) {
 // there the GEMMs need no split-K and the fp32 partials would be the largest HBM stream of the
 // add+LayerNorm kernels.  Below it the out and down projections need split-K to fill the chip
 // (at 512 rows the 16-bit form saves 8 us of add+LayerNorm per forward but costs 80 us of GEMM).
-constexpr int kBranch16Rows = 4096;
+constexpr int kBranch16Rows = kBatchedRows;
 
 // Launch plans of a slot of shape (m, b, k): GEMM tiles and split-K, attention kernel, head
 // splits.  Host arithmetic only (no allocation).
