@@ -288,10 +288,14 @@ __device__ __forceinline__ void attention_shared(const AttnArgs& a) {
   st.load(K, Vt, a.m, klo, tid);
   st.store(sK[0], sV[0], tid);
   __syncthreads();
+  // Waves past the tile's last row (the short last tile of a sequence) stage keys with the others
+  // but skip the block math: in ragged batches that is a fifth of the query slots.
+  const bool active = row0 + wave * 32 < row1;
   for (int j = 0; j < nkb; ++j) {
     const int cur = j & 1, kb = klo + j * KB;
     if (j + 1 < nkb) st.load(K, Vt, a.m, kb + KB, tid);
-    attend_block<T>(sK[cur], sV[cur], qf, o, mrow, lsum, kb, local || kb + KB > kend, qlo, qhi, lane);
+    if (active)
+      attend_block<T>(sK[cur], sV[cur], qf, o, mrow, lsum, kb, local || kb + KB > kend, qlo, qhi, lane);
     if (j + 1 < nkb) st.store(sK[cur ^ 1], sV[cur ^ 1], tid);
     __syncthreads();
   }
