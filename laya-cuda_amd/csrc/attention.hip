@@ -19,8 +19,6 @@
 //     V^T's LDS rows store keys permuted within each 16-key group to match that lane order.
 #include "kernels.hpp"
 
-#include <algorithm>
-
 namespace laya {
 
 namespace {
@@ -464,50 +462,6 @@ hipError_t launch_t(const AttnArgs& a, int mode, int waves, hipStream_t stream) 
 }  // namespace
 
 int attention_block_rows(int mode, int waves) { return mode == kAttnSplitKeys ? 32 : 32 * waves; }
-
-int build_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_seq, int m, int block,
-                          int32_t* tiles, int max_tiles) {
-  if (block <= 0 || block % 16 || max_tiles < 0) return -1;
-  int nt = 0, row = 0;
-  auto put = [&](int r0, int r1, int kstart, int klen) {
-    if (nt >= max_tiles) return false;
-    tiles[4 * nt] = r0;
-    tiles[4 * nt + 1] = r1;
-    tiles[4 * nt + 2] = kstart;
-    tiles[4 * nt + 3] = klen;
-    ++nt;
-    return true;
-  };
-  auto run = [&](int upto, int kstart, int klen) {
-    while (row < upto) {
-      const int r1 = (upto - row > block) ? row + block : upto;
-      if (!put(row, r1, kstart, klen)) return false;
-      row = r1;
-    }
-    return true;
-  };
-  for (int s = 0; s < n_seq; ++s) {
-    const int st = starts[s], len = lengths[s], e = st + (len + 15) / 16 * 16;
-    if (st % 16 || st < row || len < 0 || e > m) return -1;
-    if (!run(st, 0, -1) || !run(e, st, len)) return -1;
-  }
-  if (!run(m, 0, -1)) return -1;
-  // Longest key ranges first: workgroups start in list order, so the long tiles of a ragged batch
-  // do not end up in the last round (their cost grows with the key count).  Ties by first row: a
-  // total order, so the list is the same on every call (std::sort allocates nothing).
-  struct Quad {
-    int32_t v[4];
-  };
-  Quad* quads = reinterpret_cast<Quad*>(tiles);
-  std::sort(quads, quads + nt, [](const Quad& x, const Quad& y) {
-    return x.v[3] != y.v[3] ? x.v[3] > y.v[3] : x.v[0] < y.v[0];
-  });
-  for (int t = nt; t < max_tiles; ++t) {
-    tiles[4 * t] = tiles[4 * t + 1] = tiles[4 * t + 2] = 0;
-    tiles[4 * t + 3] = -1;
-  }
-  return nt;
-}
 
 bool attention_mode_valid(int mode, int waves) {
   if (mode == kAttnSharedKV) return waves == 1 || waves == 2 || waves == 4 || waves == 8;

@@ -100,10 +100,6 @@ struct AttnArgs {
   int m, heads, max_tiles;
   int window;  // local attention half-window (|query - key| <= window), or -1 for global
 };
-// Host: tile list of packed sequences (starts multiples of 16, increasing, spans of 16) with at
-// most `block` query rows per tile; fills all max_tiles entries, returns the used count or -1.
-int build_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_seq, int m, int block,
-                          int32_t* tiles, int max_tiles);
 // Attention kernels: kAttnSharedKV - a workgroup of `waves` waves owns 32*waves queries and stages
 // each K/V block once in LDS for all of them (large batches); kAttnSplitKeys - a workgroup owns 32
 // queries and its `waves` waves split the keys, merging at the end (few query tiles: batch 1).

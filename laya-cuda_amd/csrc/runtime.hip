@@ -21,6 +21,7 @@
 
 #include "kernels.hpp"
 #include "laya_hip.h"
+#include "packing.hpp"
 
 // Device scratch of laya_predict_static: the whole shape-slot arena of one forward (packed block,
 // activations, split-K partials, head buffers) for callers that cannot allocate.  The loader gives
@@ -109,40 +110,6 @@ struct Expected {
 int64_t geglu_row(int64_t r, int64_t f) {
   const int64_t group = r / 32, in = r % 32;
   return in < 16 ? group * 16 + in : f + group * 16 + (in - 16);
-}
-
-// Packed input layout for shape (m, b, k): the caller's block (laya_packed_ints) followed by the
-// derived work lists the host builds before the single upload.
-struct Layout {
-  size_t meta, ids, positions, rows, kinds, starts, lengths, counts, qkind, indices, user_end;
-  size_t qoff, tiles, sel_src, sel_q, n_sel, total;
-  int T, R;
-};
-Layout make_layout(int m, int b, int k) {
-  Layout L{};
-  size_t o = 0;
-  auto take = [&](size_t n) { size_t at = o; o += n; return at; };
-  auto take16 = [&](size_t n) { o = (o + 3) / 4 * 4; return take(n); };  // 16-byte aligned
-  L.meta = take(4);
-  L.ids = take(m);
-  L.positions = take(m);
-  L.rows = take(m);
-  L.kinds = take(m);
-  L.starts = take(b);
-  L.lengths = take(b);
-  L.counts = take(b);
-  L.qkind = take(b);
-  L.indices = take(static_cast<size_t>(b) * (k + 1));
-  L.user_end = o;
-  L.T = m / 16;
-  L.R = b * (k + 1);
-  L.qoff = take(b);
-  L.tiles = take16(static_cast<size_t>(4) * L.T);
-  L.sel_src = take(L.R);
-  L.sel_q = take(L.R);
-  L.n_sel = take(1);
-  L.total = o;
-  return L;
 }
 
 struct Slot {
@@ -471,46 +438,12 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
 }
 
 // Host side of Slot.fill's contract: validate the caller's block, then derive the attention tile
-// list and the compact head-row list into the same staging buffer.
+// list and the compact head-row list into the same staging buffer (packing.cpp).
 void derive_inputs(const Engine& E, Slot& s) {
-  const LayaConfig& c = E.cfg;
-  const Layout& L = s.L;
-  int32_t* P = s.h_packed;
-  const int m = s.m, b = s.b, k = s.k;
-  const int n_seq = P[L.meta], n_q = P[L.meta + 1];
-  LAYA_REQUIRE(n_seq >= 0 && n_seq <= b && n_q >= 0 && n_q <= b, "sequence/question count exceeds the shape class");
-  const int positions = E.modern ? E.rope_rows : c.max_positions;  // rows of the RoPE / position table
-  for (int i = 0; i < m; ++i) {
-    LAYA_REQUIRE(P[L.ids + i] >= 0 && P[L.ids + i] < c.vocab, "token id out of range");
-    LAYA_REQUIRE(P[L.positions + i] >= 0 && P[L.positions + i] < positions, "position out of range");
-    LAYA_REQUIRE(!E.modern || (P[L.kinds + i] >= 0 && P[L.kinds + i] < 3), "question kind out of range");
-  }
-  // Attention tiles: sequences in increasing start order, 16-aligned, non-overlapping.
-  for (int sq = 0; sq < n_seq; ++sq) {
-    const int st = P[L.starts + sq], len = P[L.lengths + sq];
-    LAYA_REQUIRE(st % 16 == 0 && len >= 0 && st + span16(len) <= m && (sq == 0 || st >= P[L.starts + sq - 1] + span16(P[L.lengths + sq - 1])),
-                 "sequences must start at increasing multiples of 16 rows and fit the shape class");
-  }
-  const int nt = build_attention_tiles(P + L.starts, P + L.lengths, n_seq, m,
-                                       attention_block_rows(s.attn_mode, s.attn_waves), P + L.tiles, s.attn_tiles);
-  LAYA_REQUIRE(nt >= 0, "attention tile list overflow");
-  // Compact head rows: per question its CLS row then its option rows.
-  int ns = 0;
-  for (int q = 0; q < n_q; ++q) {
-    const int cnt = P[L.counts + q];
-    LAYA_REQUIRE(cnt >= 0 && cnt <= k, "option count exceeds the shape class");
-    LAYA_REQUIRE(P[L.qkind + q] >= 0 && P[L.qkind + q] < 3, "question kind out of range");
-    P[L.qoff + q] = ns;
-    for (int j = 0; j <= cnt; ++j) {
-      const int src = P[L.indices + static_cast<size_t>(q) * (k + 1) + j];
-      LAYA_REQUIRE(src >= 0 && src < m, "readout index out of range");
-      P[L.sel_src + ns] = src;
-      P[L.sel_q + ns] = q;
-      ++ns;
-    }
-  }
-  for (int q = n_q; q < b; ++q) P[L.qoff + q] = ns;
-  P[L.n_sel] = ns;
+  const PackLimits lim{E.cfg.vocab, E.modern ? E.rope_rows : E.cfg.max_positions, E.modern};
+  const char* err = derive_packed(lim, s.m, s.b, s.k, s.L, s.h_packed,
+                                  attention_block_rows(s.attn_mode, s.attn_waves), s.attn_tiles);
+  if (err) throw Failure{LAYA_EINVAL, err};
 }
 
 void check_launch(hipError_t e, const char* what) {
