@@ -126,6 +126,21 @@ __device__ __forceinline__ void work_item(int nx, int ny, int* tile, int* head) 
   *tile = l - *head * nx;
 }
 
+// Workgroup -> (tile, head) over the `used` entries of the work list only (the grid covers its
+// capacity, which a ragged batch fills partly), tile-major: the list is sorted longest key range
+// first, so workgroups start in decreasing order of work across all heads, and the hardware's
+// round-robin of consecutive workgroups over the eight XCDs gives every XCD the same mix of long
+// and short items (longest-processing-time-first on each).  Returns false past the work.  With
+// equal tiles (dense batches) and 8 | heads, head h lands on XCD h % 8 for every tile, so a
+// sequence's K and V of one head are fetched into one L2.
+__device__ __forceinline__ bool work_item_used(int nx, int ny, int used, int* tile, int* head) {
+  const int id = blockIdx.x + nx * blockIdx.y;
+  if (id >= used * ny) return false;
+  *tile = id / ny;
+  *head = id - *tile * ny;
+  return true;
+}
+
 // One 64-key block of K and V^T moved from HBM to LDS by NTH cooperating threads: global loads
 // are row-contiguous 16-byte chunks (8 lanes per 128-byte row), LDS rows are 128 bytes with the
 // chunk index XOR-swizzled by kvswz(row).  V^T rows store keys permuted within each 16-key group
@@ -241,7 +256,12 @@ __device__ __forceinline__ void attention_shared(const AttnArgs& a) {
   constexpr int NT = 64 * NW;
 
   int tile, head;
-  work_item(a.max_tiles, a.heads, &tile, &head);
+  if (a.n_tiles) {
+    const int used = min(*a.n_tiles, a.max_tiles);
+    if (!work_item_used(a.max_tiles, a.heads, used, &tile, &head)) return;
+  } else {
+    work_item(a.max_tiles, a.heads, &tile, &head);
+  }
   const int4 td = reinterpret_cast<const int4*>(a.tiles)[tile];
   const int row0 = td.x, row1 = td.y, start = td.z, len = td.w;
   if (row0 >= row1) return;

@@ -99,6 +99,10 @@ struct AttnArgs {
   const int32_t* tiles;  // [max_tiles][4] = (row0, row1, kstart, klen)
   int m, heads, max_tiles;
   int window;  // local attention half-window (|query - key| <= window), or -1 for global
+  // Device count of the used entries at the front of `tiles`, or null: then the whole list is
+  // walked (unused entries exit).  With the count, the shared-K/V kernel spreads only the used
+  // entries evenly over the XCDs.
+  const int32_t* n_tiles = nullptr;
 };
 // Attention kernels: kAttnSharedKV - a workgroup of `waves` waves owns 32*waves queries and stages
 // each K/V block once in LDS for all of them (large batches); kAttnSplitKeys - a workgroup owns 32

@@ -28,6 +28,7 @@ Layout make_layout(int m, int b, int k) {
   L.sel_src = take(L.R);
   L.sel_q = take(L.R);
   L.n_sel = take(1);
+  L.n_tiles = take(1);
   L.total = o;
   return L;
 }
@@ -54,8 +55,9 @@ const char* derive_packed(const PackLimits& lim, int m, int b, int k, const Layo
       return "sequences must start at increasing multiples of 16 rows and fit the shape class";
     end = st + span16(len);
   }
-  if (build_attention_tiles(P + L.starts, P + L.lengths, n_seq, m, attn_block, P + L.tiles, attn_tiles) < 0)
-    return "attention tile list overflow";
+  const int nt = build_attention_tiles(P + L.starts, P + L.lengths, n_seq, m, attn_block, P + L.tiles, attn_tiles);
+  if (nt < 0) return "attention tile list overflow";
+  P[L.n_tiles] = nt;
   // Compact head rows: per question its CLS row then its option rows.
   int ns = 0;
   for (int q = 0; q < n_q; ++q) {

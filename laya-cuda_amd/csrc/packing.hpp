@@ -12,7 +12,7 @@ namespace laya {
 // derived work lists the host builds before the single upload.
 struct Layout {
   size_t meta, ids, positions, rows, kinds, starts, lengths, counts, qkind, indices, user_end;
-  size_t qoff, tiles, sel_src, sel_q, n_sel, total;
+  size_t qoff, tiles, sel_src, sel_q, n_sel, n_tiles, total;
   int T, R;
 };
 Layout make_layout(int m, int b, int k);

@@ -519,7 +519,8 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       check_launch(launch_gemm(g, Epi::QKV, t, s.tile[0], st), "qkv");
       break;
     case kAttention: {
-      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, m, c.heads, s.attn_tiles, ly->local ? c.window : -1};
+      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, m, c.heads, s.attn_tiles, ly->local ? c.window : -1,
+                  P + L.n_tiles};
       check_launch(launch_attention(aa, t, s.attn_mode, s.attn_waves, st), "attention");
       break;
     }
@@ -579,7 +580,7 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       check_launch(launch_gemm(g, Epi::QKV, t, s.htile[0], st), "head in_proj");
       break;
     case kHlAttention: {
-      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, m, c.heads, s.attn_tiles, -1};
+      AttnArgs aa{s.q, s.kk, s.vt, s.attn, P + L.tiles, m, c.heads, s.attn_tiles, -1, P + L.n_tiles};
       check_launch(launch_attention(aa, t, s.attn_mode, s.attn_waves, st), "head attention");
       break;
     }

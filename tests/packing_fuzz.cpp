@@ -74,6 +74,12 @@ static void check_derived(const Shape& s, const Layout& L, const int32_t* P, int
     CHECK(q[1] - q[0] <= s.block, "tile of %d rows > block %d", q[1] - q[0], s.block);
   }
   for (int r = 0; r < s.m; ++r) CHECK(cover[r] == 1, "row %d covered %d times", r, cover[r]);
+  // The used entries are the front of the list, and n_tiles counts them.
+  int used = 0;
+  while (used < nt_cap && P[L.tiles + 4 * used] < P[L.tiles + 4 * used + 1]) ++used;
+  CHECK(P[L.n_tiles] == used, "n_tiles %d != %d used entries", P[L.n_tiles], used);
+  for (int t = used; t < nt_cap; ++t)
+    CHECK(P[L.tiles + 4 * t] == P[L.tiles + 4 * t + 1], "used entry %d after an unused one", t);
   int want = 0;
   for (int q = 0; q < P[L.meta + 1]; ++q) want += P[L.counts + q] + 1;
   CHECK(P[L.n_sel] == want, "n_sel %d != %d", P[L.n_sel], want);
