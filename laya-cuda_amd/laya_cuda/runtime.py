@@ -47,7 +47,10 @@ def shape_class(sequences, questions):
 
 
 def pack(sequences, questions, key, pad, vocab=None):
-    """Packed int32 block for liblaya_hip (field order in include/laya_hip.h)."""
+    """Packed int32 block for liblaya_hip (field order in include/laya_hip.h).
+
+    Sequences are copied slice by slice; question fields are gathered in Python lists and written
+    with one NumPy scatter each (per-question NumPy calls dominated ragged batches)."""
     m, b, k = key
     size = 4 + 4 * m + 4 * b + b * (k + 1)
     block = np.zeros(size, np.int32)
@@ -55,37 +58,58 @@ def pack(sequences, questions, key, pad, vocab=None):
     ids, positions, rows, kinds = (block[o + i * m:o + (i + 1) * m] for i in range(4))
     o += 4 * m
     starts, lengths, counts, qkind = (block[o + i * b:o + (i + 1) * b] for i in range(4))
-    indices = block[o + 4 * b:].reshape(b, k + 1)
-    block[0], block[1] = len(sequences), len(questions)
+    index_base = o + 4 * b
+    indices = block[index_base:].reshape(b, k + 1)
+    n_seq, n_q = len(sequences), len(questions)
+    if n_seq > b or n_q > b:
+        raise ValueError("More sequences or questions than the shape class holds")
+    block[0], block[1] = n_seq, n_q
     ids.fill(pad)
     rows.fill(-1)
     first_kind = {}
     for seq, _, kind in questions:
         first_kind.setdefault(seq, kind)
     offset = 0
+    seq_start, seq_len = [], []
     for s, seq_ids in enumerate(sequences):
         n = len(seq_ids)
         end = offset + span(n)
+        if end > m:
+            raise ValueError("Packed sequences exceed the shape class")
         ids[offset:offset + n] = seq_ids
-        positions[offset:end] = np.arange(end - offset, dtype=np.int32)
+        positions[offset:end] = _RAMP[:end - offset] if end - offset <= _RAMP.size else np.arange(end - offset)
         rows[offset:end] = s
         kinds[offset:end] = first_kind.get(s, 0)
-        starts[s], lengths[s] = offset, n
+        seq_start.append(offset)
+        seq_len.append(n)
         offset = end
-    if offset > m:
-        raise ValueError("Packed sequences exceed the shape class")
-    for q, (s, markers, kind) in enumerate(questions):
-        if not 0 <= s < len(sequences):
-            raise ValueError(f"Question {q} names a missing sequence")
-        markers = np.asarray(markers, np.int64)
-        if len(markers) > k or (len(markers) and (markers.min() < 0 or markers.max() >= lengths[s])):
-            raise ValueError(f"Question {q} has option markers outside its sequence")
-        counts[q], qkind[q] = len(markers), kind
-        indices[q].fill(starts[s])
-        indices[q, 1:len(markers) + 1] += markers.astype(np.int32)
-    if vocab is not None and len(sequences) and (ids.min() < 0 or ids.max() >= vocab):
+    starts[:n_seq], lengths[:n_seq] = seq_start, seq_len
+    if n_q:
+        q_count, q_kind, q_first, slots, marks = [], [], [], [], []
+        for q, (s, markers, kind) in enumerate(questions):
+            if not 0 <= s < n_seq:
+                raise ValueError(f"Question {q} names a missing sequence")
+            markers = markers.tolist() if isinstance(markers, np.ndarray) else list(markers)
+            cnt = len(markers)
+            if cnt > k or (cnt and (min(markers) < 0 or max(markers) >= seq_len[s])):
+                raise ValueError(f"Question {q} has option markers outside its sequence")
+            q_count.append(cnt)
+            q_kind.append(kind)
+            q_first.append(seq_start[s])
+            base = q * (k + 1) + 1
+            slots.extend(range(base, base + cnt))
+            marks.extend(markers)
+        counts[:n_q], qkind[:n_q] = q_count, q_kind
+        indices[:n_q] = np.asarray(q_first, np.int32)[:, None]
+        if slots:
+            flat = indices.reshape(-1)
+            flat[slots] += np.asarray(marks, np.int32)
+    if vocab is not None and n_seq and (ids.min() < 0 or ids.max() >= vocab):
         raise ValueError("Token id outside the vocabulary")
     return block
+
+
+_RAMP = np.arange(1 << 16, dtype=np.int32)
 
 
 class _Resident:

@@ -81,3 +81,44 @@ def test_pack_rejects_bad_requests():
         pack([[1, 2, 3]], [(1, [1], 0)], (32, 2, 8), pad=0)
     with pytest.raises(ValueError, match="vocabulary"):
         pack([[1, 200]], [(0, [1], 0)], (32, 1, 8), pad=0, vocab=100)
+
+
+def loop_pack(sequences, questions, key, pad):
+    """Item-by-item packing of shared-sequence requests (the contract of pack, restated with plain
+    loops over tokens, rows and option slots)."""
+    m, b, k = key
+    ids, positions, rows, kinds = [pad] * m, [0] * m, [-1] * m, [0] * m
+    starts, lengths, counts, qkind = [0] * b, [0] * b, [0] * b, [0] * b
+    indices = [0] * (b * (k + 1))
+    seq_kind = {}
+    for s, _, kind in questions:
+        if s not in seq_kind:
+            seq_kind[s] = kind
+    offset = 0
+    for s, tok in enumerate(sequences):
+        for i in range(span(len(tok))):
+            if i < len(tok):
+                ids[offset + i] = int(tok[i])
+            positions[offset + i], rows[offset + i], kinds[offset + i] = i, s, seq_kind.get(s, 0)
+        starts[s], lengths[s] = offset, len(tok)
+        offset += span(len(tok))
+    for q, (s, markers, kind) in enumerate(questions):
+        counts[q], qkind[q] = len(markers), kind
+        for j in range(k + 1):
+            indices[q * (k + 1) + j] = starts[s] + (markers[j - 1] if 1 <= j <= len(markers) else 0)
+    return [len(sequences), len(questions), 0, 0] + ids + positions + rows + kinds + starts + lengths + counts + qkind + indices
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_pack_of_shared_sequences_matches_a_loop_restatement(seed):
+    """Several questions per sequence (duplicated and unsorted markers, differing kinds, sequences no
+    question names, sequences of 1 and 16k tokens): the vectorised pack equals the loops."""
+    rng = np.random.default_rng(100 + seed)
+    sequences = [rng.integers(5, 1000, int(n)).tolist() for n in rng.choice([1, 15, 16, 17, 40, 333], 6)]
+    questions = []
+    for _ in range(int(rng.integers(1, 12))):
+        s = int(rng.integers(0, len(sequences)))
+        n = len(sequences[s])
+        questions.append((s, rng.integers(0, n, int(rng.integers(0, 9))).tolist(), int(rng.integers(0, 3))))
+    key = shape_class(sequences, questions) if any(q[1] for q in questions) else (1024, 16, 8)
+    np.testing.assert_array_equal(pack(sequences, questions, key, pad=3), loop_pack(sequences, questions, key, pad=3))
