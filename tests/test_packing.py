@@ -3,7 +3,16 @@ and invariants on small inputs (no GPU)."""
 import numpy as np
 import pytest
 
+from laya_cuda import runtime
 from laya_cuda.runtime import classes, pack, shape_class, span
+
+
+@pytest.fixture(autouse=True, params=["loop", "arrays"])
+def pack_form(request, monkeypatch):
+    """Every test runs against both forms of pack (per-item loops for small requests, whole-array
+    NumPy for batches), forced by the size limit between them."""
+    monkeypatch.setattr(runtime, "PACK_LOOP_LIMIT", 1 << 30 if request.param == "loop" else -1)
+    return request.param
 
 
 def test_span_and_classes_closed_forms():
@@ -122,3 +131,28 @@ def test_pack_of_shared_sequences_matches_a_loop_restatement(seed):
         questions.append((s, rng.integers(0, n, int(rng.integers(0, 9))).tolist(), int(rng.integers(0, 3))))
     key = shape_class(sequences, questions) if any(q[1] for q in questions) else (1024, 16, 8)
     np.testing.assert_array_equal(pack(sequences, questions, key, pad=3), loop_pack(sequences, questions, key, pad=3))
+
+
+def test_pack_reports_the_first_bad_question_in_order():
+    seqs = [[5] * 10, [6] * 20]
+    marker_first = [(0, [1], 0), (1, [25], 0), (7, [1], 0)]
+    with pytest.raises(ValueError, match="Question 1 has option markers outside"):
+        pack(seqs, marker_first, (64, 4, 8), pad=0)
+    missing_first = [(0, [1], 0), (-1, [1], 0), (0, [-2], 0)]
+    with pytest.raises(ValueError, match="Question 1 names a missing sequence"):
+        pack(seqs, missing_first, (64, 4, 8), pad=0)
+    with pytest.raises(ValueError, match="Question 0 has option markers outside"):
+        pack(seqs, [(1, list(range(9)), 0)], (64, 4, 8), pad=0)  # more options than slots
+    with pytest.raises(ValueError, match="exceed the shape class"):
+        pack(seqs, [(0, [1], 0)], (16, 4, 8), pad=0)
+    with pytest.raises(ValueError, match="missing sequence"):
+        pack([], [(0, [1], 0)], (16, 1, 8), pad=0)
+
+
+def test_a_sequence_takes_the_kind_of_its_first_question():
+    seqs = [[5] * 10, [6] * 20, [7] * 3]
+    questions = [(1, [2], 2), (0, [1], 1), (1, [3], 0)]
+    m, b, k = key = (64, 4, 8)
+    kinds = pack(seqs, questions, key, pad=0)[4 + 3 * m:4 + 4 * m]
+    assert kinds[:16].tolist() == [1] * 16 and kinds[16:48].tolist() == [2] * 32
+    assert kinds[48:64].tolist() == [0] * 16  # no question names the third sequence
