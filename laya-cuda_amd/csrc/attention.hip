@@ -16,7 +16,8 @@
 //     columns).  In that accumulator layout a lane holds one query's scores for 16 keys, so
 //     the row softmax needs only one cross-lane exchange (lanes l and l^32), and the
 //     probabilities are *already* the B operand of O^T = V^T P^T: P never leaves registers.
-//     V^T's LDS rows store keys permuted within each 16-key group to match that lane order.
+//     K's LDS rows hold the keys of each 16-key group in the order 0-3, 8-11, 4-7, 12-15, which
+//     leaves each lane the scores of 8 consecutive keys, so V^T's LDS rows keep keys in order.
 #include "kernels.hpp"
 
 namespace laya {
@@ -53,8 +54,15 @@ __device__ __forceinline__ float sum2(bf16x2 p, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(p, bf16x2{static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)}, acc, false);
 }
 
+// Key order of K's LDS rows: row p of a block holds key kperm(p), bits 2 and 3 of p swapped (an
+// involution).  The S^T accumulator's element r of lane (q, g) is row 8(r/4) + 4g + r%4 of its
+// 32-key tile, i.e. key 16(r/8) + 8g + r%8: lane group g holds keys 8g..8g+7 of each 16-key group,
+// in order, exactly the k-slots it feeds the O^T = V^T P^T MFMA.
+__device__ __forceinline__ int kperm(int p) { return (p & ~12) | ((p >> 1) & 4) | ((p << 1) & 8); }
+
 // One 64-key block of the single-pass softmax for this lane's query q.  s holds the raw QK^T
-// scores of keys kb + 32kt + 8(r/4) + 4g + r%4 (the S^T accumulator layout); the reference max
+// scores of keys kb + 32kt + 16(r/8) + 8g + r%8 (the S^T accumulator layout over kperm-ordered
+// K rows); the reference max
 // `mrow` is kept in the scaled log2 domain (x * log2(e) / 8), so each probability costs one FMA
 // and one exp2.  Keys outside this lane's visible range [qlo, qhi) are masked: the sequence's end,
 // and on local layers the keys farther than the window from the query (kernels.cu:106-107).  Only
@@ -78,7 +86,7 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], fl
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int key = kb + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        const int key = kb + kt * 32 + 16 * (r >> 3) + 8 * g + (r & 7);
         const bool out = (key < qlo) | (key >= qhi);
         s[kt][r] = out ? -INFINITY : s[kt][r];
       }
@@ -141,43 +149,65 @@ __device__ __forceinline__ bool work_item_used(int nx, int ny, int used, int* ti
   return true;
 }
 
-// One 64-key block of K and V^T moved from HBM to LDS by NTH cooperating threads: global loads
-// are row-contiguous 16-byte chunks (8 lanes per 128-byte row), LDS rows are 128 bytes with the
-// chunk index XOR-swizzled by kvswz(row).  V^T rows store keys permuted within each 16-key group
-// (logical keys 4g..4g+3 and 8+4g..8+4g+3 at physical 8g..8g+7) so that a lane's 16-byte read is
-// exactly the eight keys whose probabilities the S^T accumulator leaves in that lane.
+// One 64-key block of K and V^T in LDS: 64 rows of 128 bytes each (K: one key's 64 head dims, in
+// kperm order; V^T: one head dim's 64 keys, in order), the 16-byte chunk index XOR-swizzled by
+// kvswz(row).  Thread chunk c of a block is row c / 8, physical chunk c % 8, which holds logical
+// chunk (c % 8) ^ kvswz(row).  Rows past the end of the slot are read from its last row (K) or its
+// last 8 keys (V^T) instead (branch-free loads): such keys lie past the end of every sequence, so
+// the softmax gives them probability exactly 0, and the values they read are finite values of
+// this slot.
+template <typename T>
+__device__ __forceinline__ const T* k_source(const T* K, int m, int kb, int c) {
+  const int r = c >> 3, lu = (c & 7) ^ kvswz(r);
+  return K + static_cast<size_t>(min(kb + kperm(r), m - 1)) * 64 + lu * 8;
+}
+template <typename T>
+__device__ __forceinline__ const T* v_source(const T* Vt, int m, int kb, int c) {
+  const int r = c >> 3, lu = (c & 7) ^ kvswz(r);
+  return Vt + static_cast<size_t>(r) * m + min(kb + lu * 8, m - 8);  // V^T row r = head dim
+}
+
+// Register-staged copy of a block by NTH cooperating threads (the split-key kernel's per-wave
+// stages): coalesced 16-byte global loads into registers, then 16-byte LDS stores.
 template <typename T, int NTH>
 struct KVStage {
   static constexpr int CH = KB * 8 / NTH;  // 16-byte chunks per thread per K (and per V) block
   static_assert(CH >= 1 && CH * NTH == KB * 8, "whole chunks per thread");
   i32x4 rk[CH], rv[CH];
 
-  // Rows past the end of the slot are read from its last row instead (branch-free loads): such keys
-  // lie past the end of every sequence, so the softmax gives them probability exactly 0, and the
-  // rows they read are finite values of this slot.
   __device__ __forceinline__ void load(const T* K, const T* Vt, int m, int kb, int tid) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
-      const int c = tid + NTH * i, r = c >> 3, u = c & 7;
-      const int key = min(kb + r, m - 1);
-      rk[i] = *reinterpret_cast<const i32x4*>(K + static_cast<size_t>(key) * 64 + u * 8);
-      const int k8 = min(kb + u * 8, m - 8);  // V^T row r = head dim, keys k8..k8+7
-      rv[i] = *reinterpret_cast<const i32x4*>(Vt + static_cast<size_t>(r) * m + k8);
+      rk[i] = *reinterpret_cast<const i32x4*>(k_source(K, m, kb, tid + NTH * i));
+      rv[i] = *reinterpret_cast<const i32x4*>(v_source(Vt, m, kb, tid + NTH * i));
     }
   }
   __device__ __forceinline__ void store(T* sK, T* sV, int tid) const {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
-      const int c = tid + NTH * i, r = c >> 3, u = c & 7;
-      *reinterpret_cast<i32x4*>(sK + r * 64 + ((u ^ kvswz(r)) << 3)) = rk[i];
-      const int cg = u >> 1, half = u & 1;  // keys 8u..8u+7 = half `half` of 16-key group cg
-      T* vrow = sV + r * KB;
-      const int p0 = ((2 * cg) ^ kvswz(r)) << 3, p1 = ((2 * cg + 1) ^ kvswz(r)) << 3;
-      *reinterpret_cast<int2*>(vrow + p0 + 4 * half) = make_int2(rv[i][0], rv[i][1]);
-      *reinterpret_cast<int2*>(vrow + p1 + 4 * half) = make_int2(rv[i][2], rv[i][3]);
+      const int c = tid + NTH * i;
+      *reinterpret_cast<i32x4*>(sK + c * 8) = rk[i];
+      *reinterpret_cast<i32x4*>(sV + c * 8) = rv[i];
     }
   }
 };
+
+// Direct copy of a block by NT threads (the shared-K/V kernel): global_load_lds_dwordx4, each
+// wave filling whole 1 KB runs (8 rows) of the block, so no registers or LDS store instructions
+// take part.  The caller publishes the block with publish_stage before reading it.
+template <typename T, int NT>
+__device__ __forceinline__ void kv_load_direct(const T* K, const T* Vt, int m, int kb, unsigned sk, unsigned sv,
+                                               int tid, int wave) {
+  constexpr int CH = KB * 8 / NT;
+  static_assert(CH >= 1 && CH * NT == KB * 8, "whole chunks per thread");
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int c = tid + NT * i;
+    const unsigned run = static_cast<unsigned>(wave + NT / 64 * i) * 1024u;  // this wave's 1 KB run
+    lds_load16(k_source(K, m, kb, c), sk + run);
+    lds_load16(v_source(Vt, m, kb, c), sv + run);
+  }
+}
 
 // One wave's work on one LDS-resident 64-key block for its 32 queries: S^T = K Q^T
 // (v_mfma_f32_32x32x16: keys as rows, queries as columns, so a lane holds one query's scores for
@@ -286,7 +316,9 @@ __device__ __forceinline__ void attention_shared(const AttnArgs& a) {
 
   __shared__ __align__(16) T sK[2][KB * 64];
   __shared__ __align__(16) T sV[2][64 * KB];
-  KVStage<T, NT> st;
+  const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform, for M0
+  const unsigned ldsK[2] = {lds_address(sK[0]), lds_address(sK[1])};
+  const unsigned ldsV[2] = {lds_address(sV[0]), lds_address(sV[1])};
 
   f32x16 o[2];
 #pragma unroll
@@ -303,19 +335,20 @@ __device__ __forceinline__ void attention_shared(const AttnArgs& a) {
   const int nkb = (khi - klo + KB - 1) / KB;
   const int qlo = local ? max(start, q - a.window) : start;
   const int qhi = local ? max(qlo, min(kend, q + a.window + 1)) : kend;
-  st.load(K, Vt, a.m, klo, tid);
-  st.store(sK[0], sV[0], tid);
-  __syncthreads();
+  // Double-buffered blocks: block j+1 streams into the other buffer (whose reads all ended at the
+  // previous barrier) while block j is consumed; each wave then waits for its own loads and one
+  // barrier publishes the block to all waves.
+  kv_load_direct<T, NT>(K, Vt, a.m, klo, ldsK[0], ldsV[0], tid, uwave);
+  publish_stage<waitcnt_vm(0)>();
   // Waves past the tile's last row (the short last tile of a sequence) stage keys with the others
   // but skip the block math: in ragged batches that is a fifth of the query slots.
   const bool active = row0 + wave * 32 < row1;
   for (int j = 0; j < nkb; ++j) {
     const int cur = j & 1, kb = klo + j * KB;
-    if (j + 1 < nkb) st.load(K, Vt, a.m, kb + KB, tid);
+    if (j + 1 < nkb) kv_load_direct<T, NT>(K, Vt, a.m, kb + KB, ldsK[cur ^ 1], ldsV[cur ^ 1], tid, uwave);
     if (active)
       attend_block<T>(sK[cur], sV[cur], qf, o, mrow, lsum, kb, local || kb + KB > kend, qlo, qhi, lane);
-    if (j + 1 < nkb) st.store(sK[cur ^ 1], sV[cur ^ 1], tid);
-    __syncthreads();
+    publish_stage<waitcnt_vm(0)>();
   }
 
   if (!qin) return;

@@ -67,6 +67,35 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Direct global -> LDS load (global_load_lds_dwordx4): the wave's 64 lanes each fetch 16 bytes from
+// their own address `g` and the hardware writes them, lane by lane, to the 1 KB of LDS starting at
+// byte address `lds` (wave-uniform; M0 holds it).  Issued from inline assembly: the compiler's own
+// form makes its wait-counter model assume that each such load may overwrite any LDS a pending
+// read targets, so it drains every LDS read before each load.  Here a load's destination is read
+// only after publish_stage below, which waits for the loads explicitly.  The {m0} operand lets the
+// compiler write M0 and know it is live; one s_nop separates that write from the LDS DMA.
+__device__ __forceinline__ void lds_load16(const void* g, unsigned lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds));
+}
+// Byte address of an LDS object, as M0 wants it.
+__device__ __forceinline__ unsigned lds_address(const void* p) {
+  typedef __attribute__((address_space(3))) const void* LdsPtr;
+  return static_cast<unsigned>(reinterpret_cast<uintptr_t>((LdsPtr)p));
+}
+// Publishes LDS written by direct loads: wait for this wave's memory operations up to the
+// s_waitcnt immediate `kWait`, then one workgroup barrier.  s_waitcnt and s_barrier are intrinsics
+// without memory semantics in LLVM IR, so the empty asm with a memory clobber keeps the compiler
+// from moving the following LDS reads above them; it emits no instruction.
+template <int kWait>
+__device__ __forceinline__ void publish_stage() {
+  __builtin_amdgcn_s_waitcnt(kWait);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// s_waitcnt immediate (gfx9 layout: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8) that waits
+// until at most `vm` vector memory operations are outstanding and every LDS access has completed.
+constexpr int waitcnt_vm(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
+
 template <typename T> __device__ __forceinline__ T to_half(float v) { return static_cast<T>(v); }
 template <typename T> __device__ __forceinline__ float to_float(T v) { return static_cast<float>(v); }
 

@@ -452,17 +452,6 @@ __device__ __forceinline__ int swz_k(int row) {
 // wave tiles whose accumulators alone take 256 registers: 8-wave workgroups own a CU, 4-wave ones
 // with smaller wave tiles share it with a second workgroup (whose main loop then covers this one's
 // epilogue).
-// Publishes LDS stages written by direct-to-LDS loads: wait for this wave's loads (and LDS reads)
-// up to `wait`, then one workgroup barrier.  s_waitcnt and s_barrier are intrinsics without memory
-// semantics in LLVM IR, so the empty asm with a memory clobber keeps the compiler from moving the
-// following LDS fragment reads above them; it emits no instruction.
-template <int kWait>
-__device__ __forceinline__ void publish_stage() {
-  __builtin_amdgcn_s_waitcnt(kWait);
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 template <typename T, int BM, int BN, int WM, int WN, int BKS, int S, Epi E, bool RING>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(BM * BN / (WM * WN) >= 128 * 128 ? 1 : 2)))
 void gemm_pipe_kernel(GemmArgs a) {
@@ -489,12 +478,10 @@ void gemm_pipe_kernel(GemmArgs a) {
   constexpr int kKeep = RING ? AG : NLD * (S - 2);
   constexpr int kKeepFirst = RING ? 2 * AG + BG : kFront ? NLD * (S - 1) : kKeep;  // after the prologue
   static_assert(kKeepFirst < 64, "vmcnt range");
-  // s_waitcnt vmcnt(n) lgkmcnt(0), expcnt left free (gfx9 field layout: vmcnt bits 3:0 and 15:14)
-  constexpr int kWaitSlab = (kKeep & 15) | ((kKeep >> 4) << 14) | (7 << 4);
-  constexpr int kWaitFirst = (kKeepFirst & 15) | ((kKeepFirst >> 4) << 14) | (7 << 4);
-  constexpr int kWaitAll = 7 << 4;
+  constexpr int kWaitSlab = waitcnt_vm(kKeep);
+  constexpr int kWaitFirst = waitcnt_vm(kKeepFirst);
+  constexpr int kWaitAll = waitcnt_vm(0);
   typedef typename Vec8<T>::type T8;
-  typedef __attribute__((address_space(3))) void* LdsPtr;
 
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* const lds = reinterpret_cast<T*>(smem_raw);
@@ -553,18 +540,9 @@ void gemm_pipe_kernel(GemmArgs a) {
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) early_bias[0][r4] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  // The loads are issued from inline assembly: the compiler's own global_load_lds makes its wait
-  // counter model assume each one may overwrite any LDS a pending read targets, so it drains all LDS
-  // reads before every load and serialises the fragment reads of the next k-step with the MFMAs.
-  // Here the stage a load writes is never read until after a barrier that follows an explicit
-  // s_waitcnt on those loads, so no such wait is needed.  M0 holds the LDS destination of the
-  // instruction (bound through the {m0} operand constraint, so the compiler writes it and knows it
-  // is live; one s_nop between that write and the LDS DMA that reads it).
-  const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>((LdsPtr)smem_raw));
+  const unsigned lds_base = lds_address(smem_raw);
   auto issue_at = [&](int q, int kt, int base) {  // base: element offset of the load's LDS destination
-    const T* g = src[q] + static_cast<size_t>(kt) * BKS;
-    const unsigned m0 = lds_base + static_cast<unsigned>(base + dst[q]) * 2;
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0));
+    lds_load16(src[q] + static_cast<size_t>(kt) * BKS, lds_base + static_cast<unsigned>(base + dst[q]) * 2);
   };
   auto issue = [&](int q, int kt, int st) { issue_at(q, kt, st * SLAB); };
   // Ring buffers take one operand's rows: B loads drop the A rows' offset that dst[] carries.
