@@ -135,6 +135,8 @@ def _pack_arrays(sequences, questions, m, k, ids, positions, rows, kinds, starts
     if n_q:
         qseq = np.fromiter((q[0] for q in questions), np.int64, n_q)
         qk = np.fromiter((q[2] for q in questions), np.int64, n_q)
+        if qk.min() < -2 ** 31 or qk.max() >= 2 ** 31:  # as the loop form's int32 stores refuse them
+            raise OverflowError("Question kind out of int32 range")
         cnt = np.fromiter((len(q[1]) for q in questions), np.int64, n_q)
         total = int(cnt.sum())
         marks = np.fromiter((x for q in questions for x in q[1]), np.int64, total)

@@ -156,3 +156,8 @@ def test_a_sequence_takes_the_kind_of_its_first_question():
     kinds = pack(seqs, questions, key, pad=0)[4 + 3 * m:4 + 4 * m]
     assert kinds[:16].tolist() == [1] * 16 and kinds[16:48].tolist() == [2] * 32
     assert kinds[48:64].tolist() == [0] * 16  # no question names the third sequence
+
+
+def test_pack_refuses_kinds_outside_int32():
+    with pytest.raises(OverflowError):
+        pack([[5] * 10], [(0, [1], 2 ** 32 + 1)], (64, 4, 8), pad=0)
