@@ -2,7 +2,8 @@
 //
 // Follows laya_cuda/laya.py:214-245 with no head transformer layers (laya.py:236-237), kept in
 // fp32 end to end (the returned probabilities are computed from these logits):
-//   gather  : selected = residual[indices] + type_emb[kind]   (kernels.cu:155-162; bit-exact)
+//   gather  : selected = residual[indices] + type_emb[kind]   (kernels.cu:155-162; bit-exact), the
+//             encoder's last residual + LayerNorm applied first to just those source rows
 //   scorer  : logit = w3 . gelu(W1 LN(selected; eps 1e-5) + b1) + b3   (laya.py:238-241)
 //   features: CLS row | p1, p1-p2, entropy/log(max(n,2)), max(n,2)/255  (kernels.cu:167-183)
 //   act head: acts = A2 gelu(A0 features + a0) + a2                      (laya.py:243-245)
@@ -19,7 +20,7 @@ namespace laya {
 
 namespace {
 
-template <int D>
+template <int D, typename T>
 __global__ __launch_bounds__(256) void head_gather_kernel(HeadGatherArgs a) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -27,8 +28,34 @@ __global__ __launch_bounds__(256) void head_gather_kernel(HeadGatherArgs a) {
   NormParams<D> np;
   np.load(a.gamma, a.beta, lane);
   const int src = a.sel_src[r];
+  const size_t off = static_cast<size_t>(src) * D;
   float v[D / 64];
-  load_row<D>(a.residual + static_cast<size_t>(src) * D, lane, v);
+  load_row<D>(a.residual + off, lane, v);
+  if (a.n_gamma) {  // the encoder's last residual + LayerNorm of this source row
+    NormParams<D> pn;
+    pn.load(a.n_gamma, a.n_beta, lane);
+    float br[D / 64];
+    if (a.parts) {
+      load_row<D>(a.parts + off, lane, br);
+      for (int s = 1; s < a.splits; ++s) {
+        float t[D / 64];
+        load_row<D>(a.parts + static_cast<size_t>(s) * a.part_stride + off, lane, t);
+#pragma unroll
+        for (int i = 0; i < D / 64; ++i) br[i] = br[i] + t[i];
+      }
+      if (a.bias) {
+        float t[D / 64];
+        load_row<D>(a.bias, lane, t);
+#pragma unroll
+        for (int i = 0; i < D / 64; ++i) br[i] = br[i] + t[i];
+      }
+    } else {
+      load_row16<D, T>(static_cast<const T*>(a.branch16) + off, lane, br);
+    }
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) v[i] = v[i] + br[i];
+    normalize<D>(v, pn, a.n_eps);
+  }
   if (a.type_emb) {
     float t[D / 64];
     load_row<D>(a.type_emb + static_cast<size_t>(a.qkind[a.sel_q[r]]) * D, lane, t);
@@ -255,11 +282,17 @@ __global__ __launch_bounds__(256) void act_out_kernel(ActOutArgs a) {
 
 }  // namespace
 
-hipError_t launch_head_gather(const HeadGatherArgs& a, int width, hipStream_t stream) {
+hipError_t launch_head_gather(const HeadGatherArgs& a, int width, DType t, hipStream_t stream) {
   if (a.cap <= 0) return hipSuccess;
+  if (a.n_gamma && !a.parts && !a.branch16) return hipErrorInvalidValue;
   const dim3 grid((a.cap + 3) / 4), block(256);
+  const bool h = t == DType::F16;
   switch (width) {
-#define LAYA_CASE(D) case D: LAYA_LAUNCH((head_gather_kernel<D>), grid, block, 0, stream, a); break;
+#define LAYA_CASE(D)                                                                                \
+  case D:                                                                                         \
+    if (h) LAYA_LAUNCH((head_gather_kernel<D, f16>), grid, block, 0, stream, a);               \
+    else LAYA_LAUNCH((head_gather_kernel<D, bf16>), grid, block, 0, stream, a);                \
+    break;
     LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
     LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
 #undef LAYA_CASE

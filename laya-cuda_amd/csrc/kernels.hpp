@@ -126,8 +126,20 @@ struct HeadGatherArgs {
   float* selected;  // [cap][d] gathered rows (+ type row)
   float* normed;    // [cap][d] LayerNorm of selected
   int cap;
+  // The encoder's last residual + LayerNorm, applied here to the gathered source rows only (no
+  // other row of that layer's output is read), or n_gamma null: residual already final.  The
+  // branch is the sum of `splits` fp32 partials plus `bias`, or 16-bit rows with the bias in them,
+  // added exactly as the residual+LayerNorm kernel adds them.
+  const float* parts = nullptr;
+  int splits = 0;
+  long long part_stride = 0;
+  const void* branch16 = nullptr;
+  const float* bias = nullptr;
+  const float* n_gamma = nullptr;
+  const float* n_beta = nullptr;
+  float n_eps = 0.f;
 };
-hipError_t launch_head_gather(const HeadGatherArgs& a, int width, hipStream_t stream);
+hipError_t launch_head_gather(const HeadGatherArgs& a, int width, DType t, hipStream_t stream);
 
 // Compact readout rows for the last head transformer layer: dst32[r] = src32[idx[r]] and
 // dst16[r] = src16[idx[r]] (bit-exact copies) for r < *n; rows n..cap-1 are zeroed.  Either pair

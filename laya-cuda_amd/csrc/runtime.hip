@@ -466,6 +466,9 @@ bool per_layer(int stage) { return stage >= kQkv && stage <= kFfnNorm; }
 bool per_head_layer(int stage) { return stage >= kHlQkv && stage <= kHlNorm; }
 // Whether a stage belongs to this engine's forward (for layer `layer` of its kind).
 bool stage_used(const Engine& E, int stage, int layer) {
+  // BERT-style: the last layer's residual + LayerNorm runs inside the head gather, on the gathered
+  // rows only.
+  if (stage == kFfnNorm && !E.modern && layer == E.cfg.layers - 1) return false;
   if (per_layer(stage)) return layer >= 0 && layer < E.cfg.layers;
   if (per_head_layer(stage)) {
     const int last = E.cfg.head_layers - 1;
@@ -644,9 +647,22 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       break;
     }
     case kHeadGather: {
+      // The last layer's residual + LayerNorm runs here on the gathered rows only.
+      const Layer& last = E.layers[c.layers - 1];
       HeadGatherArgs hg{s.residual, P + L.sel_src, P + L.sel_q, P + L.qkind, P + L.n_sel, E.type_emb,
                         E.s0w, E.s0b, 1e-5f, s.selected, s.normed, L.R};
-      check_launch(launch_head_gather(hg, d, st), "head gather");
+      hg.n_gamma = last.n2g;
+      hg.n_beta = last.n2b;
+      hg.n_eps = c.eps;
+      if (s.branch16) {
+        hg.branch16 = s.part;
+      } else {
+        hg.parts = s.part;
+        hg.splits = s.splits[3];
+        hg.part_stride = static_cast<long long>(md);
+        hg.bias = last.bo2;
+      }
+      check_launch(launch_head_gather(hg, d, t, st), "head gather");
       break;
     }
     case kHeadScorer: {
@@ -702,7 +718,8 @@ void forward(Engine& E, Slot& s, int marked = -1, hipEvent_t* marks = nullptr) {
   };
   run(kEmbed, 0);
   for (int i = 0; i < E.cfg.layers; ++i)
-    for (int stage = kQkv; stage <= kFfnNorm; ++stage) run(stage, i);
+    for (int stage = kQkv; stage <= kFfnNorm; ++stage)
+      if (stage_used(E, stage, i)) run(stage, i);
   if (E.modern) {
     run(kTypeNorm, 0);
     for (int j = 0; j < E.cfg.head_layers; ++j)
@@ -1432,7 +1449,7 @@ int laya_op_head_gather(const float* src, const int32_t* src_rows, const int32_t
     LAYA_REQUIRE(!type_rows || (row_question && question_kind), "type rows need the question map and kinds");
     HeadGatherArgs a{src, src_rows, row_question, question_kind, n_live, type_rows, gamma, beta, eps, selected,
                      normed, rows};
-    check_launch(launch_head_gather(a, width, static_cast<hipStream_t>(stream)), "head gather");
+    check_launch(launch_head_gather(a, width, DType::F16, static_cast<hipStream_t>(stream)), "head gather");
   });
 }
 
