@@ -187,8 +187,9 @@ int laya_attention_tiles(const int32_t* starts, const int32_t* lengths, int n_se
                          int32_t* tiles, int max_tiles);
 /* Query rows per tile of an attention kernel: mode 0 (K/V blocks staged once in LDS and shared by
  * `waves` = 1, 2, 4 or 8 waves of 32 queries each; large batches) -> 32*waves; mode 1 (one tile of
- * 32 queries whose keys are split across `waves` = 2, 4 or 8 waves; batch-1 latency) -> 32.  -1
- * for an invalid pair. */
+ * 32 queries whose keys are split across `waves` = 2, 4 or 8 waves; batch-1 latency) -> 32; mode 2
+ * (64 queries as two 32-query groups sharing each of waves/2 key groups' blocks, waves = 4 or 8;
+ * long batch-1 sequences) -> 64.  -1 for an invalid pair. */
 int laya_attention_block(int mode, int waves);
 
 /* embed (kernels.cu:16-19) fused with the embeddings norm (runtime.py:93-95):

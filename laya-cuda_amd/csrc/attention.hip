@@ -490,9 +490,137 @@ __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
   }
 }
 
+// Batch-1 sequences of 1,000+ keys: a workgroup owns 64 queries of one sequence and one head as two
+// 32-query groups, and its NW/2 key groups split the sequence's 64-key blocks (group g takes
+// blocks g, g + NW/2, ...).  The two waves of a key group (one per query group) copy its blocks
+// into one LDS region together and both read them, so each K/V byte serves 64 queries instead of
+// the split-key kernel's 32: half the K/V traffic per query, which bounds that kernel at 1,024
+// tokens.  All key groups step together (two workgroup barriers per step); the NW/2 partial (max,
+// sum, O) triples of each query group are merged through LDS.
+template <typename T, int NW>
+__global__ __launch_bounds__(64 * NW) void attention_pair_kernel(AttnArgs a) {
+  typedef typename Vec8<T>::type T8;
+  typedef typename Vec4<T>::type T4;
+  constexpr int QG = 2, KG = NW / QG, NT = 64 * NW;
+  constexpr int OP = 65;  // LDS pitch of a merged query row (floats): conflict-free column writes
+  constexpr int STAGE = 2 * KB * 64;  // per key group: one K block and one V^T block (16-bit elements)
+  constexpr size_t kStageBytes = KG * STAGE * sizeof(T), kMergeBytes = NW * 32 * OP * sizeof(float);
+
+  int tile, head;
+  work_item(a.max_tiles, a.heads, &tile, &head);
+  const int4 td = reinterpret_cast<const int4*>(a.tiles)[tile];
+  const int row0 = td.x, row1 = td.y, start = td.z, len = td.w;
+  if (row0 >= row1) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ld = a.heads * 64;
+  T* out = static_cast<T*>(a.out);
+  if (len < 0) {
+    zero_rows(out, ld, head, row0, row1, tid, NT);
+    return;
+  }
+
+  const int qg = wave % QG, kg = wave / QG;
+  const int kend = start + len;
+  const int ql = lane & 31, g = lane >> 5;
+  const int q = row0 + qg * 32 + ql;
+  const bool qin = q < row1;
+  const size_t plane = static_cast<size_t>(head) * a.m * 64;
+  const T* K = static_cast<const T*>(a.k) + plane;
+  const T* Vt = static_cast<const T*>(a.vt) + plane;
+  T8 qf[4];
+  load_q(static_cast<const T*>(a.q) + plane, q, qin, g, qf);
+
+  // Key-group staging areas during the key loop, merge area after it.
+  __shared__ __align__(16) unsigned char lds[kStageBytes > kMergeBytes ? kStageBytes : kMergeBytes];
+  __shared__ float sM[NW][32], sL[NW][32];
+  T* const sK = reinterpret_cast<T*>(lds) + kg * STAGE;
+  T* const sV = sK + KB * 64;
+  const int gt = qg * 64 + lane;  // thread index within the key group
+  KVStage<T, 64 * QG> st;
+
+  f32x16 o[2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[d][r] = 0.f;
+  float mrow = -INFINITY, lsum = 0.f;
+
+  // Key range of the tile and of this lane's query as in attention_shared.
+  const bool local = a.window >= 0;
+  const int klo = local ? max(start, (row0 - a.window) & ~15) : start;
+  const int khi = local ? min(kend, row1 + a.window) : kend;
+  const int nkb = (khi - klo + KB - 1) / KB;
+  const int qlo = local ? max(start, q - a.window) : start;
+  const int qhi = local ? max(qlo, min(kend, q + a.window + 1)) : kend;
+  const bool active = row0 + qg * 32 < row1;  // a query group past the tile's rows only stages keys
+  const int steps = (nkb + KG - 1) / KG;
+  if (kg < nkb) st.load(K, Vt, a.m, klo + KB * kg, gt);
+  for (int b = 0; b < steps; ++b) {
+    const int j = kg + KG * b;
+    if (j < nkb) st.store(sK, sV, gt);
+    __syncthreads();  // the key group's block is in LDS
+    if (j + KG < nkb) st.load(K, Vt, a.m, klo + KB * (j + KG), gt);
+    if (j < nkb && active)
+      attend_block<T>(sK, sV, qf, o, mrow, lsum, klo + KB * j, local || klo + KB * (j + 1) > kend, qlo, qhi, lane);
+    __syncthreads();  // both waves are done reading it
+  }
+
+  // Merge the key groups' partial results of each query group: O = sum_k 2^(m_k - M) O_k /
+  // sum_k 2^(m_k - M) l_k.
+  float* sO = reinterpret_cast<float*>(lds) + wave * 32 * OP;
+  const float ltot = half_sum(lsum);
+  if (g == 0) {
+    sM[wave][ql] = mrow;
+    sL[wave][ql] = ltot;
+  }
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sO[ql * OP + 32 * d + 8 * (r >> 2) + 4 * g + (r & 3)] = o[d][r];
+  __syncthreads();
+
+  constexpr int DPT = 64 * 32 * QG / NT;  // head dims per thread in the merge
+  const int mq = tid % (32 * QG), d0 = (tid / (32 * QG)) * DPT;
+  const int mg = mq / 32, mr = mq % 32, qo = row0 + mq;
+  if (qo >= row1) return;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < KG; ++k) mx = fmaxf(mx, sM[mg + QG * k][mr]);
+  float wt[KG], total = 0.f;
+#pragma unroll
+  for (int k = 0; k < KG; ++k) {
+    wt[k] = __builtin_amdgcn_exp2f(sM[mg + QG * k][mr] - mx);  // a group with no block: exp2(-inf) = 0
+    total += wt[k] * sL[mg + QG * k][mr];
+  }
+  const bool valid = qo < kend && total > 0.f;
+  const float inv = valid ? 1.0f / total : 0.f;
+  const float* merged = reinterpret_cast<const float*>(lds);
+  T* orow = out + static_cast<size_t>(qo) * ld + head * 64 + d0;
+#pragma unroll
+  for (int e = 0; e < DPT; e += 4) {
+    T4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < KG; ++k) acc += wt[k] * merged[(mg + QG * k) * 32 * OP + mr * OP + d0 + e + i];
+      v[i] = to_half<T>(valid ? acc * inv : 0.f);
+    }
+    *reinterpret_cast<T4*>(orow + e) = v;
+  }
+}
+
 template <typename T>
 hipError_t launch_t(const AttnArgs& a, int mode, int waves, hipStream_t stream) {
   const dim3 grid(a.max_tiles, a.heads);
+  if (mode == kAttnPairKeys) {
+    switch (waves) {
+      case 4: LAYA_LAUNCH((attention_pair_kernel<T, 4>), grid, dim3(256), 0, stream, a); break;
+      case 8: LAYA_LAUNCH((attention_pair_kernel<T, 8>), grid, dim3(512), 0, stream, a); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   if (mode == kAttnSplitKeys) {
     switch (waves) {
       case 2: LAYA_LAUNCH((attention_split_kernel<T, 2>), grid, dim3(128), 0, stream, a); break;
@@ -514,11 +642,14 @@ hipError_t launch_t(const AttnArgs& a, int mode, int waves, hipStream_t stream) 
 
 }  // namespace
 
-int attention_block_rows(int mode, int waves) { return mode == kAttnSplitKeys ? 32 : 32 * waves; }
+int attention_block_rows(int mode, int waves) {
+  return mode == kAttnSplitKeys ? 32 : mode == kAttnPairKeys ? 64 : 32 * waves;
+}
 
 bool attention_mode_valid(int mode, int waves) {
   if (mode == kAttnSharedKV) return waves == 1 || waves == 2 || waves == 4 || waves == 8;
   if (mode == kAttnSplitKeys) return waves == 2 || waves == 4 || waves == 8;
+  if (mode == kAttnPairKeys) return waves == 4 || waves == 8;
   return false;
 }
 

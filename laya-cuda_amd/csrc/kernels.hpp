@@ -107,7 +107,9 @@ struct AttnArgs {
 // Attention kernels: kAttnSharedKV - a workgroup of `waves` waves owns 32*waves queries and stages
 // each K/V block once in LDS for all of them (large batches); kAttnSplitKeys - a workgroup owns 32
 // queries and its `waves` waves split the keys, merging at the end (few query tiles: batch 1).
-enum AttnMode : int { kAttnSharedKV = 0, kAttnSplitKeys = 1 };
+// kAttnPairKeys - a workgroup owns 64 queries as two 32-query groups whose waves share each key
+// group's LDS-staged blocks, the waves/2 key groups splitting the keys (long batch-1 sequences).
+enum AttnMode : int { kAttnSharedKV = 0, kAttnSplitKeys = 1, kAttnPairKeys = 2 };
 int attention_block_rows(int mode, int waves);
 bool attention_mode_valid(int mode, int waves);
 hipError_t launch_attention(const AttnArgs& a, DType t, int mode, int waves, hipStream_t stream);

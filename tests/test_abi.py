@@ -143,6 +143,16 @@ def test_create_rejects_unbuilt_variants_before_touching_the_device():
     assert "64-wide" in _lib.error(None)
 
 
+def test_attention_block_rows_per_mode():
+    """Query rows per tile: shared K/V 32 x waves, split keys 32, paired query groups 64; -1 for
+    pairs a kernel does not exist for."""
+    lib = _lib.load()
+    assert [lib.laya_attention_block(0, w) for w in (1, 2, 4, 8, 3)] == [32, 64, 128, 256, -1]
+    assert [lib.laya_attention_block(1, w) for w in (1, 2, 4, 8)] == [-1, 32, 32, 32]
+    assert [lib.laya_attention_block(2, w) for w in (2, 4, 8)] == [-1, 64, 64]
+    assert lib.laya_attention_block(3, 4) == -1
+
+
 def test_device_queries():
     """laya_device_count reports zero devices (not an error) without a GPU; laya_device_info
     refuses a device that does not exist."""

@@ -358,7 +358,7 @@ def span(n):
     return -(-n // 16) * 16
 
 
-@pytest.mark.parametrize("mode,waves", [(0, 1), (0, 2), (0, 4), (0, 8), (1, 2), (1, 4), (1, 8)])
+@pytest.mark.parametrize("mode,waves", [(0, 1), (0, 2), (0, 4), (0, 8), (1, 2), (1, 4), (1, 8), (2, 4), (2, 8)])
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("lengths", [[32], [7, 96], [128, 1], [250, 131], [256, 219, 145], [500], [1024, 333]])
 def test_packed_attention_matches_float64(gpu, lengths, dtype, mode, waves):
@@ -478,7 +478,7 @@ def test_qkv_epilogue_applies_rope_to_q_and_k(gpu, tile, heads):
     np.testing.assert_allclose(from16(vt).reshape(heads, 64, M), full[:, 2].transpose(1, 2, 0), atol=3e-3, rtol=2e-3)
 
 
-@pytest.mark.parametrize("mode,waves", [(0, 2), (0, 4), (0, 8), (1, 2), (1, 4), (1, 8)])
+@pytest.mark.parametrize("mode,waves", [(0, 2), (0, 4), (0, 8), (1, 2), (1, 4), (1, 8), (2, 4), (2, 8)])
 @pytest.mark.parametrize("lengths", [[250, 131], [500], [1024, 333], [40]])
 def test_local_window_attention_matches_float64(gpu, lengths, mode, waves):
     """Local layers (kernels.cu:106-107): each query sees keys with |q - k| <= 64 of its sequence;
