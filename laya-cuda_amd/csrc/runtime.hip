@@ -361,12 +361,13 @@ void plan_slot(const Engine& E, Slot* s, int m, int b, int k) {
     s->attn_mode = kAttnSplitKeys;
     const bool one_round = static_cast<long long>((m + 31) / 32) * c.heads <= E.cus;
     s->attn_waves = !one_round ? 2 : m >= 8 * 64 ? 8 : 4;
-    // Enough 64-query tiles to occupy most CUs: pair the 32-query groups so each K/V block
-    // serves 64 queries (1,024 tokens: 11.4 against 15.8-17.2 us per launch; at 512 tokens the 96
-    // paired tiles leave half the chip idle, 7.5 against 6.3 us).
-    if (4LL * (m / 64) * c.heads >= 3LL * E.cus) {
+    // Past 512 keys a split-key wave needs more than one block: pair the 32-query groups instead,
+    // so each K/V block serves 64 queries (measured per launch, 12 heads: 640 tokens 9.0 against
+    // 12.0 us, 1,024 tokens 11.4 against 15.8, 2,048 tokens with four waves 36.0 against 37.5; at
+    // 512 tokens the split-key kernel's 6.3 us beats 7.5).
+    if (m > 8 * 64) {
       s->attn_mode = kAttnPairKeys;
-      s->attn_waves = 8;
+      s->attn_waves = m > 1536 ? 4 : 8;
     }
   }
   // Tiles of at most `block` rows: every sequence, and every run of rows between or after
