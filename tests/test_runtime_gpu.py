@@ -1,6 +1,6 @@
 """End-to-end parity of the HIP encoder path against the CPU oracle, and slot/graph lifecycle.
 
-Bar (north star): bit-exact gathers (kernel tests), max |logit - oracle| <= 1e-3 with fp32
+Bar: bit-exact gathers (kernel tests), max |logit - oracle| <= 1e-3 with fp32
 accumulation and identical argmax decisions; graph replays bit-equal to eager passes.
 """
 from pathlib import Path
