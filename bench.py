@@ -391,7 +391,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the encoder path shards by request with no collective, and "
-              "multi-GPU runs are not part of this build (use --gpus 1)", file=sys.stderr)
+              "multi-GPU runs are not implemented (use --gpus 1)", file=sys.stderr)
         sys.exit(2)
     chosen = set(args.only.split(",")) if args.only else set(WORKLOADS) | {"engine", "batching"}
     if args.calibrate_copy:
