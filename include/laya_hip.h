@@ -107,9 +107,10 @@ typedef struct LayaDevice {
   int32_t supported;        /* 1: gfx950, the architecture this library is built for */
 } LayaDevice;
 
-/* Number of HIP devices (0 without a driver or device: not an error). */
+/* Number of HIP devices (0 without a driver or device: not an error); the doctor's
+ * getDeviceCount (cli.py:140-141). */
 int laya_device_count(int* count);
-/* Properties of HIP device `device`. */
+/* Properties of HIP device `device`; the doctor's getDeviceProperties (cli.py:142-147). */
 int laya_device_info(int device, LayaDevice* out);
 
 /* Runtime(adapter, device, max_cached_shapes) construction (runtime.py:137-146). */
@@ -121,7 +122,8 @@ int laya_create(const LayaConfig* cfg, int device, int max_slots, void** handle)
 int laya_load_weight(void* handle, const char* name, const void* host_data, int host_dtype,
                      const int64_t* shape, int ndim);
 
-/* Checks that every tensor is present and resolves the layer tables.  Required before predict. */
+/* Checks that every tensor is present (the name-set check of runtime.py:149-151) and resolves the
+ * layer tables.  Required before predict. */
 int laya_finalize(void* handle);
 
 /* Runtime.predict / Slot.run (runtime.py:115-133, 171-186): find or create the shape slot (LRU
@@ -170,7 +172,9 @@ int laya_read_weight(void* handle, const char* name, float* host_out, int64_t co
 int64_t laya_used_bytes(void* handle);   /* weights + slots: CuPy pool used_bytes() */
 int laya_slot_count(void* handle);       /* len(runtime.slots) */
 int laya_destroy(void* handle);          /* Runtime.close (runtime.py:188-197) */
-const char* laya_last_error(void* handle);
+const char* laya_last_error(void* handle);  /* the exception text of ops.py:45-48, runtime.py:149-153 */
+/* No counterpart in the reference: the version of the struct layouts above, which a binding
+ * compares with the one it mirrors before it binds anything else. */
 int laya_abi_version(void);
 
 /* ------------------------------------------------------------------------------------------
