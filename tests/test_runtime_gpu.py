@@ -300,6 +300,27 @@ def test_modernbert_base_shaped_encoder_matches_oracle(gpu):
         rt.close()
 
 
+def test_modernbert_base_shaped_encoder_at_1000_tokens_matches_oracle(gpu):
+    """The same widths at the longest request a Laya checkpoint takes (max_len 1024,
+    laya.py:101-107): a 1,000-token question and a 20-token one in one pack, so the batch-1 plan
+    runs the paired split-key attention, with the +-64 window on the local layers (1, 2, 4, 5) and
+    across the whole sequence on the global ones; logits within 1e-3."""
+    spec = synthetic.modernbert_adapter(layers=6, width=768, heads=12, intermediate=1152, vocab=50368,
+                                        positions=8192, max_len=1024, head_layers=1)
+    w = synthetic.weights(spec, seed=11)
+    rng = np.random.default_rng(12)
+    items = [(list(rng.integers(5, 50368, 1000)), sorted(rng.choice(np.arange(1, 1000), 7, replace=False).tolist()), 1),
+             (list(rng.integers(5, 50368, 20)), sorted(rng.choice(np.arange(1, 20), 3, replace=False).tolist()), 0)]
+    want, want_acts = _modern_oracle(spec, w, items)
+    rt = Runtime(spec, 0, 2, weights=w)
+    try:
+        logits, acts, metrics = rt.predict(items)
+        assert metrics["shape"][0] >= 1024
+        compare(logits, acts, want, want_acts, label="modernbert 6L/768 at 1,000 tokens")
+    finally:
+        rt.close()
+
+
 def test_modernbert_rejects_mixed_types_on_a_shared_sequence(gpu):
     spec = synthetic.modernbert_adapter(layers=1, width=64, heads=1, intermediate=128, vocab=100, positions=128,
                                         max_len=64, head_layers=1)
