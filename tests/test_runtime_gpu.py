@@ -300,6 +300,30 @@ def test_modernbert_base_shaped_encoder_matches_oracle(gpu):
         rt.close()
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_batched_modernbert_matches_oracle(gpu, dtype):
+    """The ModernBERT variant in a batched slot (more than 4,096 packed rows): pre-LN layers whose
+    out/down projections reach the residual as 16-bit rows, the GeGLU and RoPE epilogues on the
+    large tiles, the LDS-shared attention with the +-64 window on local layers, and two head layers
+    over every row; nine questions of 300-1,000 tokens, each its own sequence.  Tolerances as for
+    the batch-1 workloads (fp16 1e-3, bf16 2e-3)."""
+    spec = synthetic.modernbert_adapter(layers=4, width=256, heads=4, intermediate=512, vocab=3000, positions=1024,
+                                        max_len=1024, head_layers=2, mfma_dtype=dtype)
+    w = synthetic.weights(spec, seed=13, random_norms=True)
+    rng = np.random.default_rng(14)
+    items = [(list(rng.integers(5, 3000, int(n))), sorted(rng.choice(np.arange(1, int(n)), 5, replace=False).tolist()),
+              i % 3) for i, n in enumerate(rng.integers(300, 1001, 9))]
+    want, want_acts = _modern_oracle(spec, w, items)
+    rt = Runtime(spec, 0, 2, weights=w)
+    try:
+        logits, acts, metrics = rt.predict(items)
+        assert metrics["shape"][0] >= 4096, metrics["shape"]
+        compare(logits, acts, want, want_acts, atol=LOGIT_ATOL if dtype == "float16" else 2e-3,
+                label=f"batched modernbert {dtype} rows {metrics['shape'][0]}")
+    finally:
+        rt.close()
+
+
 def test_modernbert_base_shaped_encoder_at_1000_tokens_matches_oracle(gpu):
     """The same widths at the longest request a Laya checkpoint takes (max_len 1024,
     laya.py:101-107): a 1,000-token question and a 20-token one in one pack, so the batch-1 plan
