@@ -57,3 +57,27 @@ def test_static_entry_point_matches_predict_on_consecutive_calls(gpu):
         assert rc == _lib.EINVAL and "device scratch" in _lib.error(rt._handle)
     finally:
         rt.close()
+
+
+def test_static_entry_point_matches_predict_for_modernbert(gpu):
+    """The ModernBERT variant (RoPE, GeGLU, +-64 windows on local layers, two head layers whose
+    buffers are carved from the same scratch): bit-identical to laya_predict on a 700-token pack
+    and then a smaller 90-token one."""
+    spec = synthetic.modernbert_adapter(layers=3, width=256, heads=4, intermediate=512, vocab=3000, positions=1024,
+                                        max_len=1024, head_layers=2)
+    w = synthetic.weights(spec, seed=15, random_norms=True)
+    rt = Runtime(spec, 0, 2, weights=w)
+    try:
+        rng = np.random.default_rng(16)
+        requests = [([rng.integers(5, 3000, 700, dtype=np.int32)], [(0, [3, 88, 650], 1)]),
+                    ([rng.integers(5, 3000, 60, dtype=np.int32), rng.integers(5, 3000, 30, dtype=np.int32)],
+                     [(0, [1, 2, 59], 0), (1, [5, 29], 2)])]
+        for sequences, questions in requests:
+            rc, logits, acts, metrics = static_predict(rt, sequences, questions)
+            assert rc == _lib.OK, _lib.error(rt._handle)
+            want_logits, want_acts, _ = rt.predict_sequences(sequences, questions)
+            np.testing.assert_array_equal(logits, want_logits)
+            np.testing.assert_array_equal(acts, want_acts)
+            assert np.isfinite(logits).all() and metrics.gpu_ms > 0
+    finally:
+        rt.close()
