@@ -14,11 +14,14 @@ Every workload of the metric is measured in the same run, under `workloads`:
   l1024      12L/768, 250,002-row vocabulary, 1,024 Zipf tokens, 3x5      p50/p95 latency
   ragged32   32 requests of 40-900 tokens, 1-5 questions of 4-77 options  sequences/s
   b64x1024   24L/1024, 16 heads, bf16, 64 x 1,024 tokens, 8 options each  sequences/s, MFMA fraction
-and two host-inclusive measurements:
+and three host-inclusive measurements:
   engine_predict_l512  Engine.predict on a synthetic checkpoint with a tokenizer: tokenise, pack,
                        forward, decode (the reference's definition of predict latency)
   batching             Engine serialised behind a lock vs BatchEngine, closed-loop clients
                        (1/8/32 in flight), latency percentiles, requests/s, slot-cache misses
+  modernbert_base_predict  Engine.predict at 83/512/1,024 tokens on a ModernBERT-base-shaped
+                       checkpoint (22L/768, GeGLU, windows, RoPE, one head layer; random weights):
+                       the architecture family of the real Laya checkpoints
 
 Per workload: p50/p95 of the forward's device time (events around the graph replay; inputs
 resident in HBM) and of the whole predict call (packing, H2D, replay, D2H); first_ms (slot
@@ -295,6 +298,43 @@ def run_engine_predict(path, args):
             "gpu_p50_ms": round(pct(gpu, 50), 4), "prepare_p50_ms": round(pct(prep, 50), 4)}
 
 
+def run_modernbert_predict(args):
+    """Engine.predict on a ModernBERT-base-shaped checkpoint at 83, 512 and 1,024 tokens: 22 layers,
+    d=768, 12 heads, GeGLU 1152, RoPE, global attention every third layer and +-64 windows on the
+    others, one head layer, random weights, the offline BPE tokenizer; every call tokenises, packs,
+    runs and decodes.  Real Laya checkpoints are ModernBERT/mmBERT encoders whose dimensions the
+    reference does not record, and its published predict latencies (README.md:13-16) are for those:
+    context for them, not a like-for-like comparison."""
+    from laya_cuda import Engine, synthetic
+    root = tempfile.mkdtemp(prefix="laya_bench_mb_")
+    out = {"model": "ModernBERT-base-shaped: 22L/768, 12 heads, GeGLU 1152, global every 3rd layer, +-64 windows, "
+                    "RoPE 160000/10000, one head layer, fp16 operands; random weights, BPE tokenizer trained "
+                    "offline; one 4-option choice question", "steps": args.steps}
+    try:
+        config = synthetic.modernbert_config(22, 768, 12, 1152, 50368, 8192)
+        task = dict(synthetic.task_config(1024), head_layers=1, head_max_len=64)
+        path = synthetic.checkpoint(root, config, task, seed=0, random_norms=False)[0]
+        with Engine(str(path), max_cached_shapes=4) as engine:
+            overhead = len(engine.adapter.prepare("", QUESTION)[0][0])
+            for target in (83, 512, 1024):
+                state = " refund" * max(1, target - overhead)
+                tokens = len(engine.adapter.prepare(state, QUESTION)[0][0])
+                for _ in range(args.warmup + 1):
+                    engine.predict(state, QUESTION)
+                api, gpu = [], []
+                for _ in range(args.steps):
+                    s = time.perf_counter()
+                    engine.predict(state, QUESTION)
+                    api.append((time.perf_counter() - s) * 1e3)
+                    gpu.append(engine.last_metrics["gpu_ms"])
+                out[f"tokens_{target}"] = {"tokens": tokens, "p50_ms": round(pct(api, 50), 4),
+                                           "p95_ms": round(pct(api, 95), 4), "gpu_p50_ms": round(pct(gpu, 50), 4)}
+                progress(f"modernbert-base {tokens} tokens: predict p50 {out[f'tokens_{target}']['p50_ms']} ms")
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+    return out
+
+
 def closed_loop(call, requests, clients, per_client):
     """`clients` threads, each issuing `per_client` requests one after another (a request waits
     for the previous answer of its thread): per-request latency percentiles and requests/s."""
@@ -383,7 +423,7 @@ def main():
     ap.add_argument("--stage-reps", type=int, default=10, help="eager forwards per stage for the stage timings")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="oracle time budget of the headline (0: none)")
     ap.add_argument("--only", default="", help="comma-separated subset of " + ",".join(
-        list(WORKLOADS) + ["engine", "batching"]) + " (default all; l512 is always the headline)")
+        list(WORKLOADS) + ["engine", "batching", "modernbert"]) + " (default all; l512 is always the headline)")
     ap.add_argument("--batching-requests", type=int, default=24, help="requests per closed-loop client")
     ap.add_argument("--eager", action="store_true", help="launch kernel by kernel instead of replaying hipGraphs")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -393,7 +433,7 @@ def main():
         print("bench.py measures one GPU: the encoder path shards by request with no collective, and "
               "multi-GPU runs are not implemented (use --gpus 1)", file=sys.stderr)
         sys.exit(2)
-    chosen = set(args.only.split(",")) if args.only else set(WORKLOADS) | {"engine", "batching"}
+    chosen = set(args.only.split(",")) if args.only else set(WORKLOADS) | {"engine", "batching", "modernbert"}
     if args.calibrate_copy:
         import torch
         src = torch.ones(16 << 20, dtype=torch.float32, device="cuda:0")
@@ -429,6 +469,8 @@ def main():
                 line["batching"] = run_batching(path, args)
         finally:
             shutil.rmtree(root, ignore_errors=True)
+    if "modernbert" in chosen:
+        line["modernbert_base_predict"] = run_modernbert_predict(args)
     print(json.dumps(line), flush=True)
 
 
