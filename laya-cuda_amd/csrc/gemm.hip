@@ -74,13 +74,24 @@ __device__ __forceinline__ void tile_coords(int nx, int ny, int nz, bool rows_ma
 // Bytes of LDS the epilogue stages through: one 32 x 36 fp32 (or 32 x 40 16-bit) region per wave.
 constexpr int kEpilogueStageBytes = 32 * 36 * 4;
 
+// QKV with RoPE: the position of each of this lane's output rows (one per 32-row tile), loaded at
+// kernel start.  Read in the epilogue, the position and then the cos/sin row it selects were two
+// dependent memory round trips at the end of every launch; loaded here, the position is in a
+// register long before the epilogue and only the table read remains there.  The load is older
+// than every operand load of the main loop, so its waits cover it.
+template <int TM, Epi E>
+__device__ __forceinline__ void load_early_pos(const GemmArgs& a, int row, int (&pos)[TM]) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) pos[i] = E == Epi::QKV_ROPE ? a.positions[min(row + i * 32, a.M - 1)] : 0;
+}
+
 // Epilogue shared by both GEMM kernels: acc holds this wave's (BM/WM) x (BN/WN) block of C^T as
 // 32x32 MFMA tiles; smem_raw must have kEpilogueStageBytes per wave free (the caller's main loop is
 // done with LDS: its last barrier has passed).
 template <typename T, int BM, int BN, int WM, int WN, Epi E, bool kEarlyBias>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
                                               const float4 (&early_bias)[kEarlyBias ? BN / WN / 32 : 1][4],
-                                              int m0, int n0, int z,
+                                              const int (&early_pos)[BM / WM / 32], int m0, int n0, int z,
                                               unsigned char* smem_raw, int lane, int wave) {
   constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
@@ -169,20 +180,26 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[B
         const int col0 = n0 + wn0 + j * 32;
         emit_rows(i, h, [&](int row, int col) { return out + static_cast<long long>(row) * a.ldo + col0 + col; });
       }
-  } else if constexpr (E == Epi::QKV) {
+  } else if constexpr (E == Epi::QKV || E == Epi::QKV_ROPE) {
     T* const vt = static_cast<T*>(a.vt);
+    // RoPE on Q and K (rotate-half, the reference's `layout`, kernels.cu:73-77) on the fp32
+    // accumulator before the single rounding: tiles j and j+1 hold dims d and d+32 of one head.  The
+    // cos/sin values of this lane's rows (dims 8 r4 + 4 kg .. +3 of each row's position) are all
+    // read before the first tile is emitted: one memory round trip instead of one per row tile.
+    constexpr bool rope = E == Epi::QKV_ROPE;
+    float4 rcos[rope ? TM : 1][4], rsin[rope ? TM : 1][4];
+    if constexpr (rope) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const size_t at = static_cast<size_t>(early_pos[i]) * 32 + 8 * r4 + 4 * kg;
+          rcos[i][r4] = *reinterpret_cast<const float4*>(a.rope_cos + at);
+          rsin[i][r4] = *reinterpret_cast<const float4*>(a.rope_sin + at);
+        }
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      const int row_lane = rbase + i * 32 + lrow;
-      // RoPE on Q and K (rotate-half, the reference's `layout`, kernels.cu:73-77) on the fp32
-      // accumulator before the single rounding: tiles j and j+1 hold dims d and d+32 of one head.
-      const float* cs = nullptr;
-      const float* sn = nullptr;
-      if (a.rope_cos) {
-        const int pos = a.positions[min(row_lane, a.M - 1)];
-        cs = a.rope_cos + static_cast<size_t>(pos) * 32;
-        sn = a.rope_sin + static_cast<size_t>(pos) * 32;
-      }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int col0 = n0 + wn0 + j * 32;
@@ -192,21 +209,21 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[B
           auto qdst = [&](int d0) {
             return [=](int row, int col) { return qk + static_cast<size_t>(row) * 64 + d0 + col; };
           };
-          if (cs) {
+          if constexpr (rope) {
             if (j & 1) continue;  // emitted with its pair
             if constexpr (TN >= 2) {
               T4 lo[4], hi[4];
 #pragma unroll
               for (int r4 = 0; r4 < 4; ++r4) {
-                const int dim = 8 * r4 + 4 * kg;
                 float v0[4], v1[4];
                 take(i, j, r4, v0);
                 take(i, j + 1, r4, v1);
+                const float c4[4] = {rcos[i][r4].x, rcos[i][r4].y, rcos[i][r4].z, rcos[i][r4].w};
+                const float s4[4] = {rsin[i][r4].x, rsin[i][r4].y, rsin[i][r4].z, rsin[i][r4].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                  const float c = cs[dim + e], sv = sn[dim + e];
-                  lo[r4][e] = to_half<T>(v0[e] * c - v1[e] * sv);
-                  hi[r4][e] = to_half<T>(v1[e] * c + v0[e] * sv);
+                  lo[r4][e] = to_half<T>(v0[e] * c4[e] - v1[e] * s4[e]);
+                  hi[r4][e] = to_half<T>(v1[e] * c4[e] + v0[e] * s4[e]);
                 }
               }
               emit_rows(i, lo, qdst(0));
@@ -342,6 +359,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
       early_bias[0][r4] = with_bias ? *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + 8 * r4 + 4 * kg)
                                  : make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  int early_pos[TM];
+  load_early_pos<TM, E>(a, m0 + wm0 + lrow, early_pos);
   // One 64-deep slab from LDS buffer `buf`: four 16-deep MFMA steps.  With at most 8 MFMA tiles per
   // wave the fragments are double-buffered in registers, so the LDS reads of step kk+1 are in
   // flight while the MFMAs of step kk run; larger wave tiles have no registers to spare for that.
@@ -414,7 +433,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_kernel(GemmArgs a) {
     __syncthreads();  // the epilogue reuses LDS
   }
 
-  gemm_epilogue<T, BM, BN, WM, WN, E, kEarlyBias>(a, acc, early_bias, m0, n0, z, smem_raw, lane, wave);
+  gemm_epilogue<T, BM, BN, WM, WN, E, kEarlyBias>(a, acc, early_bias, early_pos, m0, n0, z, smem_raw, lane, wave);
 }
 
 // LDS layout of the pipelined kernel: rows of BKS 16-bit elements, CPR = BKS / 8 chunks of 16 B per
@@ -540,6 +559,8 @@ void gemm_pipe_kernel(GemmArgs a) {
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) early_bias[0][r4] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
+  int early_pos[TM];
+  load_early_pos<TM, E>(a, m0 + wm0 + (lane & 31), early_pos);
   const unsigned lds_base = lds_address(smem_raw);
   auto issue_at = [&](int q, int kt, int base) {  // base: element offset of the load's LDS destination
     lds_load16(src[q] + static_cast<size_t>(kt) * BKS, lds_base + static_cast<unsigned>(base + dst[q]) * 2);
@@ -684,7 +705,7 @@ void gemm_pipe_kernel(GemmArgs a) {
   // reuses LDS.
   __builtin_amdgcn_s_waitcnt(kWaitAll);
   __syncthreads();
-  gemm_epilogue<T, BM, BN, WM, WN, E, kEarlyBias>(a, acc, early_bias, m0, n0, z, smem_raw, lane, wave);
+  gemm_epilogue<T, BM, BN, WM, WN, E, kEarlyBias>(a, acc, early_bias, early_pos, m0, n0, z, smem_raw, lane, wave);
 }
 
 struct TileDef {
@@ -812,6 +833,7 @@ hipError_t set_lds_all() {
   if (e == hipSuccess) e = set_lds_attr<T, Epi::HALF>();
   if (e == hipSuccess) e = set_lds_attr<T, Epi::GELU>();
   if (e == hipSuccess) e = set_lds_attr<T, Epi::QKV>();
+  if (e == hipSuccess) e = set_lds_attr<T, Epi::QKV_ROPE>();
   if (e == hipSuccess) e = set_lds_attr<T, Epi::RELU>();
   if (e == hipSuccess) e = set_lds_attr<T, Epi::GEGLU>();
   return e;
@@ -916,10 +938,12 @@ hipError_t launch_gemm(const GemmArgs& args, Epi epi, DType t, int tile, hipStre
   if (a.M <= 0) return hipSuccess;
   if (a.K % BK || a.N % kTiles[tile].bn || a.splits < 1) return hipErrorInvalidValue;
   if (epi != Epi::F32 && a.splits != 1) return hipErrorInvalidValue;
+  if (epi == Epi::QKV_ROPE && !a.rope_cos) return hipErrorInvalidValue;
+  if (epi == Epi::QKV && a.rope_cos) epi = Epi::QKV_ROPE;
   // RoPE needs both halves of a head in one lane: wave tiles of 64-column multiples.
   const TileDef& td = kTiles[tile];
-  if (epi == Epi::QKV && a.rope_cos && (td.bn / td.wn) % 64) return hipErrorInvalidValue;
-  if (epi == Epi::QKV && a.M % 8) return hipErrorInvalidValue;  // V^T is stored in runs of 8 tokens
+  if (epi == Epi::QKV_ROPE && (td.bn / td.wn) % 64) return hipErrorInvalidValue;
+  if ((epi == Epi::QKV || epi == Epi::QKV_ROPE) && a.M % 8) return hipErrorInvalidValue;  // V^T: runs of 8 tokens
   if (epi == Epi::GEGLU && (a.N % 32 || a.ldo * 2 < a.N)) return hipErrorInvalidValue;
   if (epi == Epi::F32 && a.splits != 1 && a.bias) return hipErrorInvalidValue;  // bias joins the sum later
   const bool h = t == DType::F16;
@@ -928,6 +952,8 @@ hipError_t launch_gemm(const GemmArgs& args, Epi epi, DType t, int tile, hipStre
     case Epi::HALF: return h ? launch_t<f16, Epi::HALF>(a, tile, stream) : launch_t<bf16, Epi::HALF>(a, tile, stream);
     case Epi::GELU: return h ? launch_t<f16, Epi::GELU>(a, tile, stream) : launch_t<bf16, Epi::GELU>(a, tile, stream);
     case Epi::QKV: return h ? launch_t<f16, Epi::QKV>(a, tile, stream) : launch_t<bf16, Epi::QKV>(a, tile, stream);
+    case Epi::QKV_ROPE:
+      return h ? launch_t<f16, Epi::QKV_ROPE>(a, tile, stream) : launch_t<bf16, Epi::QKV_ROPE>(a, tile, stream);
     case Epi::RELU: return h ? launch_t<f16, Epi::RELU>(a, tile, stream) : launch_t<bf16, Epi::RELU>(a, tile, stream);
     case Epi::GEGLU: return h ? launch_t<f16, Epi::GEGLU>(a, tile, stream) : launch_t<bf16, Epi::GEGLU>(a, tile, stream);
   }

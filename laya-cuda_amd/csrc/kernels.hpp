@@ -46,7 +46,9 @@ hipError_t launch_embed(const EmbedArgs& a, int width, DType t, hipStream_t stre
 hipError_t launch_add_norm(const AddNormArgs& a, int width, DType t, hipStream_t stream);
 
 // ---- MFMA GEMM: out[M][N] = A[M][K] * B[N][K]^T (+ bias), fp32 accumulate ----
-enum class Epi : int { F32 = 0, HALF = 1, GELU = 2, QKV = 3, RELU = 4, GEGLU = 5 };
+// QKV_ROPE is the QKV epilogue with RoPE compiled in: launch_gemm picks it for Epi::QKV when rope
+// tables are given, so the QKV kernels without RoPE carry none of its code.
+enum class Epi : int { F32 = 0, HALF = 1, GELU = 2, QKV = 3, RELU = 4, GEGLU = 5, QKV_ROPE = 6 };
 
 struct GemmArgs {
   const void* a;  // [M][lda] 16-bit
