@@ -7,11 +7,12 @@
 // Workgroup: 4 or 8 waves on a WM x WN grid; each wave owns (BM/WM) x (BN/WN) made of 32x32 MFMA
 // tiles (8 waves put two waves on each SIMD of the CU, so one issues MFMAs while the other waits on
 // LDS or a barrier).  Two main loops share one epilogue:
-//   gemm_kernel       small tiles (batch-1 problems): 64-deep K slabs staged through registers into
-//                     two LDS buffers, PF slabs of global loads in flight;
-//   gemm_pipe_kernel  large tiles (batched problems): an S-stage pipeline of K slabs loaded straight
-//                     from global memory into LDS, LDS fragment reads of the next k-step overlapped
-//                     with the MFMAs of the current one.
+//   gemm_kernel       register-staged tiles: 64-deep K slabs staged through registers into two LDS
+//                     buffers, PF slabs of global loads in flight;
+//   gemm_pipe_kernel  an S-stage pipeline of K slabs loaded straight from global memory into LDS,
+//                     LDS fragment reads of the next k-step overlapped with the MFMAs of the current
+//                     one: deep pipelines of small tiles for batch-1 problems, and for batched
+//                     problems large tiles, the 256x256 ones with a ring of half-slab buffers.
 // LDS rows hold one slab row with the 16-byte chunk index XOR-swizzled (swz, swz_k below), so the
 // lanes reading one k-chunk of consecutive rows hit distinct banks.
 //
@@ -21,8 +22,12 @@
 //          residual+LayerNorm kernel that consumes it);
 //   HALF - + bias, rounded to 16-bit;
 //   GELU - + bias, exact-erf GELU, rounded to 16-bit (FFN up);
+//   RELU - + bias, ReLU, rounded to 16-bit (FFN up of the head layers);
+//   GEGLU - gelu(gate) * value of the gate/value rows interleaved in 32-row groups, rounded to
+//          16-bit, N/2 wide (ModernBERT FFN up);
 //   QKV  - + bias, rounded, written head-major: Q,K [h][M][64] and V transposed [h][64][M]
-//          (replaces the reference's separate `layout` pass, kernels.cu:68-82).
+//          (replaces the reference's separate `layout` pass, kernels.cu:68-82);
+//   QKV_ROPE - QKV with rotate-half RoPE applied to Q and K in fp32 before the rounding.
 #include "kernels.hpp"
 
 #include <type_traits>
