@@ -11,7 +11,8 @@
 //     listed by the host so no tile straddles sequences (ragged batches waste no key blocks);
 //   * NW waves, each owning 32 queries; K and V^T blocks of 64 keys are staged through LDS,
 //     double-buffered, and shared by the waves (large batches), or - for batch-1 requests with few
-//     query tiles - the NW waves of a 32-query tile split the keys and merge their partial results;
+//     query tiles - the NW waves of a 32-query tile split the keys and merge their partial results
+//     (past 512 keys two 32-query groups share each staged block, halving the K/V reads per query);
 //   * the wave computes S^T = K Q^T with v_mfma_f32_32x32x16 (keys as rows, queries as
 //     columns).  In that accumulator layout a lane holds one query's scores for 16 keys, so
 //     the row softmax needs only one cross-lane exchange (lanes l and l^32), and the
