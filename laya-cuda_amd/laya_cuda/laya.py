@@ -20,6 +20,40 @@ from .models import read_json
 
 TYPES = ("choice", "score", "noul")
 
+# Tokenizer stages that act character by character or only split (never join text across a split),
+# and the pre-tokenizers among them that always split in front of a space that follows a letter or
+# digit.  With such a configuration, and no added token containing whitespace, the ids of a text cut
+# at such a space are a prefix of the ids of the whole text.
+_LOCAL_NORMALIZERS = {"NFC", "NFD", "NFKC", "NFKD", "Lowercase", "Strip", "StripAccents", "BertNormalizer"}
+_SPLITS_AT_SPACES = {"Whitespace", "WhitespaceSplit", "BertPreTokenizer"}
+_LOCAL_PRE_TOKENIZERS = _SPLITS_AT_SPACES | {"Digits", "Punctuation", "UnicodeScripts", "ByteLevel", "Metaspace"}
+
+
+def _splits_at_spaces(config):
+    """True when the serialised tokenizer ``config`` (tokenizer.json) encodes every cut of a text in
+    front of a space that follows a letter or digit as a prefix of the whole text's ids."""
+    def normalizer_ok(n):
+        if n is None:
+            return True
+        if n.get("type") == "Sequence":
+            return all(normalizer_ok(m) for m in n.get("normalizers", []))
+        return n.get("type") in _LOCAL_NORMALIZERS
+
+    def splits(p):
+        t = p.get("type")
+        return (t in _SPLITS_AT_SPACES or (t == "ByteLevel" and p.get("use_regex", True))
+                or (t == "Metaspace" and p.get("split", True)))
+
+    pre = config.get("pre_tokenizer")
+    if pre is None or not normalizer_ok(config.get("normalizer")):
+        return False
+    parts = pre.get("pretokenizers", []) if pre.get("type") == "Sequence" else [pre]
+    if not parts or not all(p.get("type") in _LOCAL_PRE_TOKENIZERS for p in parts) or not any(map(splits, parts)):
+        return False
+    if config.get("model", {}).get("type") not in ("BPE", "WordPiece", "WordLevel", "Unigram"):
+        return False
+    return not any(any(c.isspace() for c in a.get("content", "")) for a in config.get("added_tokens", []))
+
 
 def text(value):
     return value if isinstance(value, str) else json.dumps(value, ensure_ascii=False, default=str)
@@ -167,6 +201,7 @@ class Laya(EncoderSpec):
         self.tokenizer = Tokenizer.from_file(str(path / "tokenizer/tokenizer.json"))
         self.tokenizer.no_padding()
         self.tokenizer.no_truncation()
+        self.prefix_cut = _splits_at_spaces(json.loads(self.tokenizer.to_str()))
         specials = {}
         for name in ("tokenizer_config.json", "special_tokens_map.json"):
             if (path / "tokenizer" / name).is_file():
@@ -185,13 +220,36 @@ class Laya(EncoderSpec):
     def from_configs(cls, config, task, pad=0):
         """Adapter without files (synthetic checkpoints fed pre-tokenised ids): no ``prepare``."""
         self = object.__new__(cls)
-        self.path, self.cfg, self.config, self.tokenizer = None, task, config, None
+        self.path, self.cfg, self.config, self.tokenizer, self.prefix_cut = None, task, config, None, False
         EncoderSpec.__init__(self, config, task)
         self.pad = pad
         return self
 
     def encode(self, value):
         return self.tokenizer.encode(value.replace(self.mask_text, " "), add_special_tokens=False).ids
+
+    def state_ids(self, text):
+        """The state text's ids as far as prepare can use them: at least the first max_len of the
+        whole text's.  The reference encodes the whole state and keeps its first max_len - 3 or
+        fewer ids (laya.py:110-130); a long state costs the tokenizer time for every character.
+        Where the tokenizer splits in front of a space that follows a letter or digit
+        (``prefix_cut``), a prefix of the text cut there encodes to a prefix of the whole text's
+        ids, so a prefix of 6 x max_len characters (doubled while it yields fewer than max_len
+        ids) gives the same first max_len ids."""
+        encode = self.tokenizer.encode
+        if self.prefix_cut:
+            chars = 6 * self.max_len
+            while chars < len(text):
+                cut = text.find(" ", chars)
+                while cut > 0 and not text[cut - 1].isalnum():
+                    cut = text.find(" ", cut + 1)
+                if cut <= 0:
+                    break
+                ids = encode(text[:cut], add_special_tokens=False).ids
+                if len(ids) >= self.max_len:
+                    return ids
+                chars = 2 * cut
+        return encode(text, add_special_tokens=False).ids
 
     def prepare(self, state, questions):
         """Token ids, option marker positions and type per question (laya.py:104-135)."""
@@ -205,12 +263,12 @@ class Laya(EncoderSpec):
             texts.append(f"{kind} question: {instruction}")
             texts.extend(" " + option for option in options)
         texts = [t.replace(self.mask_text, " ") for t in texts]
+        state_ids = self.state_ids(texts[0])
         if len(texts) >= 12:
-            encoded = [e.ids for e in self.tokenizer.encode_batch(texts, add_special_tokens=False)]
+            encoded = [e.ids for e in self.tokenizer.encode_batch(texts[1:], add_special_tokens=False)]
         else:
-            encoded = [self.tokenizer.encode(t, add_special_tokens=False).ids for t in texts]
-        cursor = iter(encoded)
-        state_ids, items = next(cursor), []
+            encoded = [self.tokenizer.encode(t, add_special_tokens=False).ids for t in texts[1:]]
+        cursor, items = iter(encoded), []
         for qid, (kind, _, _, options) in zip(questions, parsed):
             head = next(cursor)
             opts = [[self.mask] + next(cursor)[:48] for _ in options]

@@ -114,3 +114,110 @@ def test_options_keep_at_most_48_tokens(laya, monkeypatch):
     assert first == [laya.mask] + enc(laya, " long: " + long_text)[:48]
     assert second == [laya.mask] + enc(laya, " short")
     assert markers[0] - 2 == len(enc(laya, "choice question: route the ticket"))  # 120 - 51 tokens leave room
+
+
+# ---- the state encoded from a prefix: the same first max_len ids as the whole text -------------
+
+def _trained(pre_tokenizer, normalizer=None, model="bpe"):
+    """A tokenizer trained here on the checkpoint corpus with the given pipeline stages."""
+    from tokenizers import Tokenizer, models, trainers
+    from laya_cuda import synthetic
+    if model == "wordpiece":
+        tok = Tokenizer(models.WordPiece(unk_token="[UNK]"))
+        trainer = trainers.WordPieceTrainer(vocab_size=400, special_tokens=synthetic.TOKENIZER_SPECIALS)
+    else:
+        tok = Tokenizer(models.BPE(unk_token="[UNK]"))
+        trainer = trainers.BpeTrainer(vocab_size=400, special_tokens=synthetic.TOKENIZER_SPECIALS)
+    if normalizer is not None:
+        tok.normalizer = normalizer
+    if pre_tokenizer is not None:
+        tok.pre_tokenizer = pre_tokenizer
+    tok.train_from_iterator(synthetic.TOKENIZER_CORPUS * 10, trainer)
+    return tok
+
+
+def _pipelines():
+    from tokenizers import normalizers, pre_tokenizers
+    return {
+        "whitespace": _trained(pre_tokenizers.Whitespace()),
+        "byte-level": _trained(pre_tokenizers.ByteLevel(add_prefix_space=False)),
+        "metaspace": _trained(pre_tokenizers.Metaspace()),
+        "bert": _trained(pre_tokenizers.BertPreTokenizer(), normalizers.BertNormalizer(lowercase=True),
+                         model="wordpiece"),
+        "nfkc-sequence": _trained(pre_tokenizers.Sequence([pre_tokenizers.WhitespaceSplit(),
+                                                           pre_tokenizers.Digits(individual_digits=True)]),
+                                  normalizers.Sequence([normalizers.NFKC(), normalizers.Lowercase()])),
+    }
+
+
+def _random_text(rng, words):
+    pieces = ["refund", "the", "customer", "payment", "délivery", "naïve", "ﬁle", "ÉCOLE", "12345", "3.5%",
+              "don't", "e-mail", "软件错误", "😀", "ünïcödé", "[MASK]", "(note)", "—", "a", "x" * 40]
+    seps = [" ", " ", " ", "  ", "\t", "\n", " \n ", ", ", ". ", "", "   "]
+    return "".join(pieces[rng.integers(len(pieces))] + seps[rng.integers(len(seps))] for _ in range(words))
+
+
+def test_state_prefix_encodes_to_the_whole_texts_leading_ids():
+    """For every pipeline whose pre-tokenizer splits in front of a space after a letter or digit,
+    the state ids prepare uses (the first max_len) are those of the whole text, on random texts of
+    mixed scripts, digits, punctuation, runs of whitespace and an added-token string."""
+    import json
+    import numpy as np
+    from laya_cuda.laya import _splits_at_spaces
+
+    class Spec:
+        pass
+
+    rng = np.random.default_rng(7)
+    for name, tok in _pipelines().items():
+        assert _splits_at_spaces(json.loads(tok.to_str())), name
+        for max_len in (16, 128, 512, 1024):
+            spec = Spec()
+            spec.tokenizer, spec.max_len, spec.prefix_cut = tok, max_len, True
+            for words in (3, 200, 3000):
+                text = _random_text(rng, words)
+                whole = tok.encode(text, add_special_tokens=False).ids
+                ids = Laya.state_ids(spec, text)
+                # every id of the prefix's encoding, up to the cut, is the whole text's
+                assert len(ids) >= min(max_len, len(whole)) and ids == whole[:len(ids)], (name, max_len, words)
+
+
+def test_state_prefix_cut_is_off_for_tokenizers_that_join_across_spaces():
+    """No pre-tokenizer (the whole text is one piece), a normaliser that rewrites patterns, or an
+    added token containing a space: the whole text is encoded."""
+    import json
+    from tokenizers import AddedToken, normalizers, pre_tokenizers
+    from laya_cuda.laya import _splits_at_spaces
+    assert not _splits_at_spaces(json.loads(_trained(None).to_str()))
+    assert not _splits_at_spaces(json.loads(_trained(pre_tokenizers.Whitespace(),
+                                                     normalizers.Replace(" ", "_")).to_str()))
+    assert not _splits_at_spaces(json.loads(_trained(pre_tokenizers.Punctuation()).to_str()))
+    tok = _trained(pre_tokenizers.Whitespace())
+    tok.add_tokens([AddedToken("late delivery")])
+    assert not _splits_at_spaces(json.loads(tok.to_str()))
+
+
+def test_prepare_is_unchanged_by_the_prefix_cut(laya):
+    """prepare with the prefix cut equals prepare encoding the whole state, for long states."""
+    import numpy as np
+    rng = np.random.default_rng(9)
+    assert laya.prefix_cut
+    for words in (10, 400, 5000):
+        state = _random_text(rng, words)
+        fast = laya.prepare(state, QUESTIONS)
+        laya.prefix_cut = False
+        try:
+            slow = laya.prepare(state, QUESTIONS)
+        finally:
+            laya.prefix_cut = True
+        assert fast == slow
+
+
+def test_a_cut_inside_a_word_breaks_the_prefix_property():
+    """The check above can fail: cutting "refund" after "ref" encodes a different last token."""
+    tok = _pipelines()["byte-level"]
+    text = "refund " * 200
+    whole = tok.encode(text, add_special_tokens=False).ids
+    bad = tok.encode(text[:7 * 100 + 3], add_special_tokens=False).ids
+    good = tok.encode(text[:7 * 100 + 6], add_special_tokens=False).ids
+    assert bad != whole[:len(bad)] and good == whole[:len(good)]
