@@ -22,16 +22,17 @@ TYPES = ("choice", "score", "noul")
 
 # Tokenizer stages that act character by character or only split (never join text across a split),
 # and the pre-tokenizers among them that always split in front of a space that follows a letter or
-# digit.  With such a configuration, and no added token containing whitespace, the ids of a text cut
-# at such a space are a prefix of the ids of the whole text.
-_LOCAL_NORMALIZERS = {"NFC", "NFD", "NFKC", "NFKD", "Lowercase", "Strip", "StripAccents", "BertNormalizer"}
+# digit.  With such a configuration, and no added token that contains whitespace or strips the
+# whitespace after it, a text cut at such spaces encodes piece by piece to the ids of the whole text:
+# each piece after the first starts with that space exactly as it does inside the whole text.
+_LOCAL_NORMALIZERS = {"NFC", "NFD", "NFKC", "NFKD", "Lowercase", "StripAccents", "BertNormalizer"}
 _SPLITS_AT_SPACES = {"Whitespace", "WhitespaceSplit", "BertPreTokenizer"}
 _LOCAL_PRE_TOKENIZERS = _SPLITS_AT_SPACES | {"Digits", "Punctuation", "UnicodeScripts", "ByteLevel", "Metaspace"}
 
 
 def _splits_at_spaces(config):
-    """True when the serialised tokenizer ``config`` (tokenizer.json) encodes every cut of a text in
-    front of a space that follows a letter or digit as a prefix of the whole text's ids."""
+    """True when the serialised tokenizer ``config`` (tokenizer.json) encodes a text cut in front of
+    spaces that follow a letter or digit, piece by piece, to the whole text's ids."""
     def normalizer_ok(n):
         if n is None:
             return True
@@ -52,7 +53,8 @@ def _splits_at_spaces(config):
         return False
     if config.get("model", {}).get("type") not in ("BPE", "WordPiece", "WordLevel", "Unigram"):
         return False
-    return not any(any(c.isspace() for c in a.get("content", "")) for a in config.get("added_tokens", []))
+    return not any(a.get("rstrip") or any(c.isspace() for c in a.get("content", ""))
+                   for a in config.get("added_tokens", []))
 
 
 def text(value):
@@ -229,27 +231,27 @@ class Laya(EncoderSpec):
         return self.tokenizer.encode(value.replace(self.mask_text, " "), add_special_tokens=False).ids
 
     def state_ids(self, text):
-        """The state text's ids as far as prepare can use them: at least the first max_len of the
-        whole text's.  The reference encodes the whole state and keeps its first max_len - 3 or
-        fewer ids (laya.py:110-130); a long state costs the tokenizer time for every character.
+        """The state text's ids as far as prepare can use them: the whole text's, or at least their
+        first max_len.  The reference encodes the whole state and keeps its first max_len - 3 or
+        fewer ids (laya.py:110-130), so a long state costs the tokenizer time for every character.
         Where the tokenizer splits in front of a space that follows a letter or digit
-        (``prefix_cut``), a prefix of the text cut there encodes to a prefix of the whole text's
-        ids, so a prefix of 6 x max_len characters (doubled while it yields fewer than max_len
-        ids) gives the same first max_len ids."""
+        (``prefix_cut``), the text is encoded in pieces cut at such spaces, the first about 6 x
+        max_len characters, each next one sized for the ids still missing, until max_len ids are
+        there: the pieces' ids joined are the whole text's, and the work never exceeds encoding
+        the whole text."""
         encode = self.tokenizer.encode
-        if self.prefix_cut:
-            chars = 6 * self.max_len
-            while chars < len(text):
-                cut = text.find(" ", chars)
-                while cut > 0 and not text[cut - 1].isalnum():
-                    cut = text.find(" ", cut + 1)
-                if cut <= 0:
-                    break
-                ids = encode(text[:cut], add_special_tokens=False).ids
-                if len(ids) >= self.max_len:
-                    return ids
-                chars = 2 * cut
-        return encode(text, add_special_tokens=False).ids
+        if not self.prefix_cut:
+            return encode(text, add_special_tokens=False).ids
+        ids, start, chars = [], 0, 6 * self.max_len
+        while start < len(text) and len(ids) < self.max_len:
+            end = text.find(" ", start + chars)
+            while end > 0 and not text[end - 1].isalnum():
+                end = text.find(" ", end + 1)
+            end = end if end > 0 else len(text)
+            ids += encode(text[start:end], add_special_tokens=False).ids
+            start = end
+            chars = (self.max_len - len(ids)) * start // max(len(ids), 1) * 5 // 4 + 64
+        return ids
 
     def prepare(self, state, questions):
         """Token ids, option marker positions and type per question (laya.py:104-135)."""

@@ -195,6 +195,12 @@ def test_state_prefix_cut_is_off_for_tokenizers_that_join_across_spaces():
     tok = _trained(pre_tokenizers.Whitespace())
     tok.add_tokens([AddedToken("late delivery")])
     assert not _splits_at_spaces(json.loads(tok.to_str()))
+    # pieces after the first start with a space: a normaliser that strips it, or an added token
+    # that swallows the space after it, would encode that space differently from the whole text
+    assert not _splits_at_spaces(json.loads(_trained(pre_tokenizers.ByteLevel(), normalizers.Strip()).to_str()))
+    tok = _trained(pre_tokenizers.ByteLevel())
+    tok.add_tokens([AddedToken("refund9", rstrip=True)])
+    assert not _splits_at_spaces(json.loads(tok.to_str()))
 
 
 def test_prepare_is_unchanged_by_the_prefix_cut(laya):
@@ -221,3 +227,35 @@ def test_a_cut_inside_a_word_breaks_the_prefix_property():
     bad = tok.encode(text[:7 * 100 + 3], add_special_tokens=False).ids
     good = tok.encode(text[:7 * 100 + 6], add_special_tokens=False).ids
     assert bad != whole[:len(bad)] and good == whole[:len(good)]
+
+
+def test_state_pieces_join_to_the_whole_texts_ids():
+    """Texts whose first piece yields fewer than max_len ids are encoded in several pieces (each
+    after the first starting with the space it was cut at); the joined ids are the whole text's."""
+    import numpy as np
+
+    class Counting:
+        def __init__(self, tok):
+            self.tok, self.calls = tok, 0
+
+        def encode(self, text, add_special_tokens=False):
+            self.calls += 1
+            return self.tok.encode(text, add_special_tokens=add_special_tokens)
+
+    class Spec:
+        pass
+
+    rng = np.random.default_rng(11)
+    for name, tok in _pipelines().items():
+        for text in ("refund " * 3000, "refund  payment\t" * 1500, " ".join(["x" * 40] * 400) + " end",
+                     _random_text(rng, 4000).replace("软件错误", "refund")):
+            for max_len in (512, 1024):
+                spec = Spec()
+                spec.tokenizer, spec.max_len, spec.prefix_cut = Counting(tok), max_len, True
+                whole = tok.encode(text, add_special_tokens=False).ids
+                ids = Laya.state_ids(spec, text)
+                assert len(ids) >= min(max_len, len(whole)) and ids == whole[:len(ids)], (name, max_len)
+        spec = Spec()
+        spec.tokenizer, spec.max_len, spec.prefix_cut = Counting(tok), 1024, True
+        Laya.state_ids(spec, "refund " * 3000)
+        assert spec.tokenizer.calls >= 2, name  # the several-piece path ran
