@@ -324,6 +324,30 @@ def test_batched_modernbert_matches_oracle(gpu, dtype):
         rt.close()
 
 
+def test_large_batched_modernbert_matches_oracle(gpu):
+    """A batched slot past 12,288 packed rows, where the out and down projections may run on
+    hipBLASLt's kernels (chosen by timing when the slot is created; ModernBERT's have no bias):
+    eighteen questions of 500-1,000 tokens, fp16 logits within 1e-3 of the oracle, and the graph
+    replay equal to the eager forward bit for bit."""
+    spec = synthetic.modernbert_adapter(layers=3, width=256, heads=4, intermediate=512, vocab=3000, positions=1024,
+                                        max_len=1024, head_layers=1)
+    w = synthetic.weights(spec, seed=17, random_norms=True)
+    rng = np.random.default_rng(18)
+    items = [(list(rng.integers(5, 3000, int(n))), sorted(rng.choice(np.arange(1, int(n)), 4, replace=False).tolist()),
+              i % 3) for i, n in enumerate(rng.integers(500, 1001, 18))]
+    want, want_acts = _modern_oracle(spec, w, items)
+    rt = Runtime(spec, 0, 2, weights=w)
+    try:
+        logits, acts, metrics = rt.predict(items)
+        assert metrics["shape"][0] >= 12288 and metrics["graph_replay"], metrics["shape"]
+        eager = rt.predict(items, capture=False)
+        np.testing.assert_array_equal(eager[0], logits)
+        np.testing.assert_array_equal(eager[1], acts)
+        compare(logits, acts, want, want_acts, label=f"batched modernbert rows {metrics['shape'][0]}")
+    finally:
+        rt.close()
+
+
 def test_modernbert_base_shaped_encoder_at_1000_tokens_matches_oracle(gpu):
     """The same widths at the longest request a Laya checkpoint takes (max_len 1024,
     laya.py:101-107): a 1,000-token question and a 20-token one in one pack, so the batch-1 plan
