@@ -20,6 +20,7 @@
 //     K's LDS rows hold the keys of each 16-key group in the order 0-3, 8-11, 4-7, 12-15, which
 //     leaves each lane the scores of 8 consecutive keys, so V^T's LDS rows keep keys in order.
 #include "kernels.hpp"
+#include <type_traits>
 
 namespace laya {
 
@@ -34,11 +35,20 @@ constexpr int KB = 64;  // keys per block
 // the same banks).
 __device__ __forceinline__ int kvswz(int row) { return (row >> 1) & 7; }
 
+// max(a, b, c) in one v_max3_f32.  Written out because fmaxf chains over MFMA results compile to
+// a v_max_f32 x, x (NaN quieting) per input before the combining instructions: 31 instructions for
+// a 32-score block maximum instead of 16.  The scores are never NaN (masked keys are -inf).
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // Combine a value with the one held by lane l ^ 32 (the other half of the S^T accumulator's k-slots
 // for the same query) with v_permlane32_swap: a VALU lane exchange, no LDS round trip.
 __device__ __forceinline__ float half_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max3(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float half_sum(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -92,12 +102,14 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], fl
         s[kt][r] = out ? -INFINITY : s[kt][r];
       }
   }
-  float mx[4] = {s[0][0], s[0][1], s[0][2], s[0][3]};
+  // Block maximum of the lane's 32 scores: two chains of v_max3 (16 instructions).
+  float mx[2] = {max3(s[0][0], s[0][1], s[0][2]), max3(s[1][0], s[1][1], s[1][2])};
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mx[r & 3] = fmaxf(mx[r & 3], s[kt][r]);
-  float bmax = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+    for (int r = 3; r < 15; r += 2) mx[kt] = max3(mx[kt], s[kt][r], s[kt][r + 1]);
+  float bmax = max3(mx[0], s[0][15], s[1][15]);
+  bmax = max3(bmax, mx[1], mx[1]);
   bmax = half_max(bmax) * c;
   const bool grow = bmax > mrow + kSlack;  // false while everything seen so far is masked
   if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -210,25 +222,35 @@ __device__ __forceinline__ void kv_load_direct(const T* K, const T* Vt, int m, i
   }
 }
 
+// This lane's fragment reads in a staged block, as element offsets from the block's first row:
+// row ql, logical chunk 2i + g (k-step i) at its swizzled position.  The lane's other rows are 32
+// rows (2,048 elements) further on and the same chunk positions (kvswz(ql + 32) = kvswz(ql)), and a
+// block's V^T rows follow its K rows (KB * 64 elements), so every fragment read of a block is one
+// of these four addresses plus a constant: the reads carry it as their immediate offset.
+__device__ __forceinline__ void fragment_offsets(int lane, int (&off)[4]) {
+  const int ql = lane & 31, g = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) off[i] = ql * 64 + (((2 * i + g) ^ kvswz(ql)) << 3);
+}
+
 // One wave's work on one LDS-resident 64-key block for its 32 queries: S^T = K Q^T
 // (v_mfma_f32_32x32x16: keys as rows, queries as columns, so a lane holds one query's scores for
-// 16 keys), the online-softmax step, and O^T += V^T P^T with P straight from registers.
+// 16 keys), the online-softmax step, and O^T += V^T P^T with P straight from registers.  frag[i]
+// is the block's first K row plus fragment_offsets' offset i (V^T rows follow the K rows).
 template <typename T>
-__device__ __forceinline__ void attend_block(const T* sK, const T* sV, const typename Vec8<T>::type (&qf)[4],
+__device__ __forceinline__ void attend_block(const T* const (&frag)[4], const typename Vec8<T>::type (&qf)[4],
                                              f32x16 (&o)[2], float& mrow, float& lsum, int kb, bool edge, int qlo,
                                              int qhi, int lane) {
   typedef typename Vec8<T>::type T8;
-  const int ql = lane & 31, g = lane >> 5;
+  const int g = lane >> 5;
   f32x16 s[2];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
-    const int kr = kt * 32 + ql;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const int ch = 2 * ks + g;
-      const T8 kf = *reinterpret_cast<const T8*>(sK + kr * 64 + ((ch ^ kvswz(kr)) << 3));
+      const T8 kf = *reinterpret_cast<const T8*>(frag[ks] + kt * 32 * 64);
       s[kt] = mfma32(kf, qf[ks], s[kt]);
     }
   }
@@ -245,8 +267,7 @@ __device__ __forceinline__ void attend_block(const T* sK, const T* sV, const typ
     rs[1] = sum2(__builtin_shufflevector(pb, pb, 6, 7), rs[1]);
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
-      const int vr = d * 32 + ql;
-      const T8 vf = *reinterpret_cast<const T8*>(sV + vr * KB + (((2 * c + g) ^ kvswz(vr)) << 3));
+      const T8 vf = *reinterpret_cast<const T8*>(frag[c] + KB * 64 + d * 32 * KB);
       o[d] = mfma32(vf, pb, o[d]);
     }
   }
@@ -315,11 +336,20 @@ __device__ __forceinline__ void attention_shared(const AttnArgs& a) {
   T8 qf[4];
   load_q(static_cast<const T*>(a.q) + plane, q, qin, g, qf);
 
-  __shared__ __align__(16) T sK[2][KB * 64];
-  __shared__ __align__(16) T sV[2][64 * KB];
+  // Two block buffers, each K's rows then V^T's rows.
+  __shared__ __align__(16) T skv[2][2 * KB * 64];
   const int uwave = __builtin_amdgcn_readfirstlane(wave);  // wave-uniform, for M0
-  const unsigned ldsK[2] = {lds_address(sK[0]), lds_address(sK[1])};
-  const unsigned ldsV[2] = {lds_address(sV[0]), lds_address(sV[1])};
+  const unsigned ldsK[2] = {lds_address(skv[0]), lds_address(skv[1])};
+  const unsigned ldsV[2] = {lds_address(skv[0] + KB * 64), lds_address(skv[1] + KB * 64)};
+  int off[4];
+  fragment_offsets(lane, off);
+  const T* frag0[4];
+  const T* frag1[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    frag0[i] = skv[0] + off[i];
+    frag1[i] = skv[1] + off[i];
+  }
 
   f32x16 o[2];
 #pragma unroll
@@ -344,12 +374,19 @@ __device__ __forceinline__ void attention_shared(const AttnArgs& a) {
   // Waves past the tile's last row (the short last tile of a sequence) stage keys with the others
   // but skip the block math: in ragged batches that is a fifth of the query slots.
   const bool active = row0 + wave * 32 < row1;
-  for (int j = 0; j < nkb; ++j) {
-    const int cur = j & 1, kb = klo + j * KB;
+  // Block j from buffer cur (a constant in each copy of the step, so the fragment reads keep fixed
+  // addresses) while block j+1 streams into the other buffer.
+  auto step = [&](int j, auto cur_c) {
+    constexpr int cur = decltype(cur_c)::value;
+    const int kb = klo + j * KB;
     if (j + 1 < nkb) kv_load_direct<T, NT>(K, Vt, a.m, kb + KB, ldsK[cur ^ 1], ldsV[cur ^ 1], tid, uwave);
     if (active)
-      attend_block<T>(sK[cur], sV[cur], qf, o, mrow, lsum, kb, local || kb + KB > kend, qlo, qhi, lane);
+      attend_block<T>(cur ? frag1 : frag0, qf, o, mrow, lsum, kb, local || kb + KB > kend, qlo, qhi, lane);
     publish_stage<waitcnt_vm(0)>();
+  };
+  for (int j = 0; j < nkb; j += 2) {
+    step(j, std::integral_constant<int, 0>());
+    if (j + 1 < nkb) step(j + 1, std::integral_constant<int, 1>());
   }
 
   if (!qin) return;
@@ -440,10 +477,15 @@ __global__ __launch_bounds__(64 * NW) void attention_split_kernel(AttnArgs a) {
   if (wave < nkb) st.load(K, Vt, a.m, klo + KB * wave, lane);
   T* const sK = mine;
   T* const sV = mine + KB * 64;
+  int off[4];
+  fragment_offsets(lane, off);
+  const T* frag[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) frag[i] = sK + off[i];
   for (int j = wave; j < nkb; j += NW) {
     st.store(sK, sV, lane);
     if (j + NW < nkb) st.load(K, Vt, a.m, klo + KB * (j + NW), lane);
-    attend_block<T>(sK, sV, qf, o, mrow, lsum, klo + KB * j, local || klo + KB * (j + 1) > kend, qlo, qhi, lane);
+    attend_block<T>(frag, qf, o, mrow, lsum, klo + KB * j, local || klo + KB * (j + 1) > kend, qlo, qhi, lane);
   }
 
   // Merge the waves' partial results: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w.
@@ -555,6 +597,11 @@ __global__ __launch_bounds__(64 * NW) void attention_pair_kernel(AttnArgs a) {
   const int qhi = local ? max(qlo, min(kend, q + a.window + 1)) : kend;
   const bool active = row0 + qg * 32 < row1;  // a query group past the tile's rows only stages keys
   const int steps = (nkb + KG - 1) / KG;
+  int off[4];
+  fragment_offsets(lane, off);
+  const T* frag[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) frag[i] = sK + off[i];
   if (kg < nkb) st.load(K, Vt, a.m, klo + KB * kg, gt);
   for (int b = 0; b < steps; ++b) {
     const int j = kg + KG * b;
@@ -562,7 +609,7 @@ __global__ __launch_bounds__(64 * NW) void attention_pair_kernel(AttnArgs a) {
     __syncthreads();  // the key group's block is in LDS
     if (j + KG < nkb) st.load(K, Vt, a.m, klo + KB * (j + KG), gt);
     if (j < nkb && active)
-      attend_block<T>(sK, sV, qf, o, mrow, lsum, klo + KB * j, local || klo + KB * (j + 1) > kend, qlo, qhi, lane);
+      attend_block<T>(frag, qf, o, mrow, lsum, klo + KB * j, local || klo + KB * (j + 1) > kend, qlo, qhi, lane);
     __syncthreads();  // both waves are done reading it
   }
 
