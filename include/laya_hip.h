@@ -150,7 +150,7 @@ int laya_predict_static(void* handle, const int32_t* host_packed, const LayaShap
 /* Per-launch timing, the native counterpart of the reference's profiling hook that records events
  * around every Ops.call/linear (tools/profile_long.py:21-67).  The forward is a fixed list of
  * stages (embed_norm; per layer qkv, attention, attn_out, attn_norm, ffn_up, ffn_down, ffn_norm;
- * head_gather, head_scorer, head_logit, head_features, act_hidden, act_out).  laya_time_stage uploads the request like
+ * head_gather, head_scorer, head_tail).  laya_time_stage uploads the request like
  * laya_predict, runs one eager forward so every buffer holds this request's values, then launches
  * stage `stage` of layer `layer` `reps` times back to back between two events on the engine's
  * stream and stores the average per launch in *avg_ms.  Stages that normalise in place

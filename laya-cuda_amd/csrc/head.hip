@@ -10,9 +10,12 @@
 //
 // Only the head rows that exist are computed: the host lists them compactly (question by
 // question: CLS, then each option), so a slot whose option capacity is padded to a power of two
-// does no work for the padding.  Launches: gather+LN, scorer.1 (fp32 MFMA, split-K), scorer tail
-// (a wave per row), features (a workgroup per question), act_head.0 (the same fp32 MFMA GEMM over
-// all questions, K padded with zeros to a multiple of 256 so it splits 8-16 ways), act output.
+// does no work for the padding.  Launches: gather+LN; one launch of the fp32 MFMA GEMM for both
+// scorer.1 (split-K) and the CLS-row columns of act_head.0 (every input of the act head but the
+// four features, which depend on the logits); the tail, a workgroup per question (its logits,
+// features, the act head's four feature columns, GELU and output layer).  Three dependent launches
+// where each stage of laya.py:238-245 was one: the work is a few microseconds of memory round
+// trips, so the launch count sets the head's latency.
 #include "kernels.hpp"
 #include "rowops.hpp"
 
@@ -95,13 +98,14 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(GatherRowsArgs a) {
 // Workgroup tile 32 rows x 64 cols, 4 waves of 16x32.  The split's K range is staged in LDS up to
 // 128 columns at a time, every 16-byte load of a chunk issued before the first LDS store, so a
 // split of up to 128 columns costs one memory round trip (these tiny products are all latency).
-__global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
+__device__ __forceinline__ void head_gemm_tile(const HeadGemmArgs& a, int bx, int by, int z) {
   constexpr int BM = 32, BN = 64, KC = 128, KP = KC + 4;  // pitch KP: 16-byte rows, conflict-free reads
   constexpr int AV = BM * KC / 4 / 256, BV = BN * KC / 4 / 256;  // float4 loads per thread per chunk
   // The live row count is a device scalar of this request; it is only consulted for the stores,
   // so its load does not delay the operand loads (rows up to the capacity are in the buffers).
   const int n_rows = *a.n_rows;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN, z = blockIdx.z;
+  const int m0 = by * BM, n0 = bx * BN;
+  const int ldx = a.ldx ? a.ldx : a.K, ldw = a.ldw ? a.ldw : a.K;
   if (m0 >= a.cap) return;
   // Row blocks past the live rows exit at once (ragged batches fill a small part of their
   // capacity); the first row block never waits for the count, so batch-1 launches keep their
@@ -114,6 +118,14 @@ __global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
   const int per = a.K / a.splits;  // a multiple of 32
   const int kb = z * per, ke = kb + per;
   f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  // Source row of each of this thread's A loads (the same in every chunk); a mapped row costs one
+  // index load before the first chunk.
+  int xr[AV];
+#pragma unroll
+  for (int i = 0; i < AV; ++i) {
+    const int rr = min(m0 + (tid + 256 * i) / (KC / 4), a.cap - 1);
+    xr[i] = a.x_rows ? min(max(a.x_rows[rr], 0), a.x_cap - 1) : rr;
+  }
   for (int k0 = kb; k0 < ke; k0 += KC) {
     const int kn = min(KC, ke - k0);
     // Chunk loads, all in flight together: rows past the capacity and columns past the split read
@@ -121,14 +133,13 @@ __global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
     f32x4 ra[AV], rb[BV];
 #pragma unroll
     for (int i = 0; i < AV; ++i) {
-      const int e = tid + 256 * i, r = e / (KC / 4), c = 4 * (e % (KC / 4));
-      const int rr = min(m0 + r, a.cap - 1), cc = min(c, kn - 4);
-      ra[i] = *reinterpret_cast<const f32x4*>(a.x + static_cast<size_t>(rr) * a.K + k0 + cc);
+      const int e = tid + 256 * i, c = 4 * (e % (KC / 4));
+      ra[i] = *reinterpret_cast<const f32x4*>(a.x + static_cast<size_t>(xr[i]) * ldx + k0 + min(c, kn - 4));
     }
 #pragma unroll
     for (int i = 0; i < BV; ++i) {
       const int e = tid + 256 * i, r = e / (KC / 4), c = 4 * (e % (KC / 4));
-      rb[i] = *reinterpret_cast<const f32x4*>(a.w + static_cast<size_t>(n0 + r) * a.K + k0 + min(c, kn - 4));
+      rb[i] = *reinterpret_cast<const f32x4*>(a.w + static_cast<size_t>(n0 + r) * ldw + k0 + min(c, kn - 4));
     }
 #pragma unroll
     for (int i = 0; i < AV; ++i) {
@@ -160,123 +171,164 @@ __global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmArgs a) {
     }
 }
 
-// Scorer tail, one wave per compact head row (CLS or option): logit = w3 . gelu(v + b1) + b3.
+// Workgroups of two independent products in one flat grid: the first `blocks0` ids walk product 0
+// (column block fastest, then row block, then split), the rest product 1.
+struct HeadGemmPair {
+  HeadGemmArgs g0, g1;
+  int blocks0;
+};
+int head_gemm_blocks(const HeadGemmArgs& a) { return (a.N / 64) * ((a.cap + 31) / 32) * a.splits; }
+__global__ __launch_bounds__(256) void head_gemm_kernel(HeadGemmPair p) {
+  auto run = [](const HeadGemmArgs& a, int id) {
+    const int nx = a.N / 64, ny = (a.cap + 31) / 32;
+    head_gemm_tile(a, id % nx, (id / nx) % ny, id / (nx * ny));
+  };
+  const int id = blockIdx.x;
+  if (id < p.blocks0) run(p.g0, id);
+  else run(p.g1, id - p.blocks0);
+}
+
+// Head tail, one workgroup (8 waves) per question slot.  Everything that does not depend on the
+// logits is loaded first: each thread's act_head.0 output (its CLS-row partials summed in split
+// order, its four feature weights, its bias) and each wave's act_head.2 row.  Then the question's
+// CLS and option rows' logits (a wave per row: scorer.1 partials summed in split order, + b1, GELU,
+// dot w3, + b3) go to LDS and the logits output; wave 0 takes the softmax statistics of the option
+// logits (the four features); every thread finishes its act_head.0 outputs (+ the feature columns,
+// GELU) into LDS, and each wave takes act outputs (dot with act_head.2's row, + a2).
+constexpr int kTailThreads = 512, kTailWaves = kTailThreads / 64;
+constexpr int kTailHidden = 256;  // act_head.0 outputs whose inputs are prefetched (one per thread)
 template <int D>
-__global__ __launch_bounds__(256) void head_logit_kernel(HeadLogitArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= a.cap) return;
-  const int n_sel = *a.n_sel;  // consulted only before the stores (rows up to the capacity exist)
-  const size_t off = static_cast<size_t>(r) * D;
+__global__ __launch_bounds__(kTailThreads) void head_tail_kernel(HeadTailArgs a) {
+  extern __shared__ float tl[];  // row logits [k+1] | features [4] | act hidden [hidden]
+  float* const zl = tl;
+  float* const fv = tl + a.k + 1;
+  float* const hid = fv + 4;
+  const int q = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float* const logits = a.logits + static_cast<size_t>(q) * (a.k + 1);
+  float* const acts = a.acts + static_cast<size_t>(q) * a.n_act;
+  const int n_q = *a.n_q;
+  // act_head.0 output `tid` (the first kTailHidden outputs) and act_head.2 row `wave`, prefetched.
+  auto act_partial = [&](int o) {
+    const size_t off = static_cast<size_t>(q) * a.hidden + o;
+    float v = 0.f;  // CLS-row partials in split order, eight loads in flight per group
+    for (int s0 = 0; s0 < a.asplits; s0 += 8) {
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = a.aparts[min(s0 + u, a.asplits - 1) * a.asplit_stride + off];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v = s0 + u < a.asplits ? v + t[u] : v;
+    }
+    return v;
+  };
+  const int po = min(tid, a.hidden - 1);
+  const float pv = act_partial(po), pb = a.a0b[po];
+  const float4 pw = *reinterpret_cast<const float4*>(a.a0w + static_cast<size_t>(po) * a.a0_ld + D);
+  constexpr int HR = kTailHidden / 64;  // act_head.2 values per lane of the prefetched row
+  float w2[HR];
+  {
+    const float* w = a.a2w + static_cast<size_t>(min(wave, a.n_act - 1)) * a.hidden;
+#pragma unroll
+    for (int j = 0; j < HR; ++j) w2[j] = w[min(lane + 64 * j, a.hidden - 1)];
+  }
+  if (q >= n_q) {  // unused question slots of the shape class (the prefetches above stay in bounds)
+    for (int j = tid; j <= a.k; j += kTailThreads) logits[j] = 0.f;
+    for (int j = tid; j < a.n_act; j += kTailThreads) acts[j] = 0.f;
+    return;
+  }
+
+  const int count = a.counts[q], base = a.qoff[q];
   float b1[D / 64], w3[D / 64];
   load_row<D>(a.b1, lane, b1);
   load_row<D>(a.w3, lane, w3);
-  // Partials summed in split order; loaded four at a time (clamped to the last split, whose copies
-  // are not added) so each group costs one memory round trip instead of one per split.
-  float v[D / 64];
+  constexpr int G = D <= 1024 ? 8 : 4;  // scorer.1 partials in flight per group
+  for (int r = wave; r <= count; r += kTailWaves) {
+    const size_t off = static_cast<size_t>(base + r) * D;
+    // Partials loaded G at a time (clamped to the last split, whose copies are not added): one
+    // memory round trip per group instead of one per split.
+    float v[D / 64];
 #pragma unroll
-  for (int i = 0; i < D / 64; ++i) v[i] = 0.f;
-  for (int s0 = 0; s0 < a.splits; s0 += 4) {
-    float t[4][D / 64];
+    for (int i = 0; i < D / 64; ++i) v[i] = 0.f;
+    for (int s0 = 0; s0 < a.splits; s0 += G) {
+      float t[G][D / 64];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) load_row<D>(a.parts + min(s0 + u, a.splits - 1) * a.split_stride + off, lane, t[u]);
+      for (int u = 0; u < G; ++u) load_row<D>(a.parts + min(s0 + u, a.splits - 1) * a.split_stride + off, lane, t[u]);
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < G; ++u)
 #pragma unroll
-      for (int i = 0; i < D / 64; ++i) v[i] = s0 + u < a.splits ? v[i] + t[u][i] : v[i];
-  }
-  float dot = 0.f;
+        for (int i = 0; i < D / 64; ++i) v[i] = s0 + u < a.splits ? v[i] + t[u][i] : v[i];
+    }
+    float dot = 0.f;
 #pragma unroll
-  for (int i = 0; i < D / 64; ++i) dot += gelu(v[i] + b1[i]) * w3[i];
-  const float logit = wave_sum(dot) + a.b3[0];
-  if (r >= n_sel) return;
-  if (lane == 0) {
-    const int q = a.sel_q[r];
-    a.row_logit[r] = logit;
-    a.logits[static_cast<size_t>(q) * (a.k + 1) + (r - a.qoff[q])] = logit;
-  }
-}
-
-// One workgroup per question slot: softmax statistics over its option logits (slots 1..count),
-// written with its CLS row as the act head's input row (zero-padded to kp columns).
-__global__ __launch_bounds__(256) void head_features_kernel(HeadFeatureArgs a) {
-  const int q = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float* logits = a.logits + static_cast<size_t>(q) * (a.k + 1);
-  float* feat = a.feat + static_cast<size_t>(q) * a.kp;
-  if (q >= *a.n_q) {  // unused question slots of the shape class
-    for (int j = tid; j <= a.k; j += 256) logits[j] = 0.f;
-    for (int j = tid; j < a.kp; j += 256) feat[j] = 0.f;
-    for (int j = tid; j < a.n_act; j += 256) a.acts[static_cast<size_t>(q) * a.n_act + j] = 0.f;
-    return;
-  }
-  const int count = a.counts[q], base = a.qoff[q];
-  for (int j = count + 1 + tid; j <= a.k; j += 256) logits[j] = 0.f;
-  for (int e = tid; e < a.width; e += 256) feat[e] = a.selected[static_cast<size_t>(base) * a.width + e];
-  for (int e = a.width + 4 + tid; e < a.kp; e += 256) feat[e] = 0.f;
-  if (wave != 0) return;
-  const float* z = a.row_logit + base + 1;
-  float mx = -INFINITY;
-  for (int j = lane; j < count; j += 64) mx = fmaxf(mx, z[j]);
-  mx = wave_max(mx);
-  float se = 0.f;
-  for (int j = lane; j < count; j += 64) se += expf(z[j] - mx);
-  se = wave_sum(se);
-  float ent = 0.f, t1 = 0.f, t2 = 0.f;  // entropy and the two largest probabilities
-  for (int j = lane; j < count; j += 64) {
-    const float p = expf(z[j] - mx) / se;
-    ent -= p * logf(fmaxf(p, 1e-9f));
-    if (p > t1) {
-      t2 = t1;
-      t1 = p;
-    } else {
-      t2 = fmaxf(t2, p);
+    for (int i = 0; i < D / 64; ++i) dot += gelu(v[i] + b1[i]) * w3[i];
+    const float logit = wave_sum(dot) + a.b3[0];
+    if (lane == 0) {
+      zl[r] = logit;
+      logits[r] = logit;
     }
   }
-  ent = wave_sum(ent);
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const float o1 = __shfl_xor(t1, d, 64), o2 = __shfl_xor(t2, d, 64);
-    t2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
-    t1 = fmaxf(t1, o1);
-  }
-  if (lane == 0) {
-    const int n = max(count, 2);
-    feat[a.width] = t1;
-    feat[a.width + 1] = t1 - t2;
-    feat[a.width + 2] = ent / logf(static_cast<float>(n));
-    feat[a.width + 3] = static_cast<float>(n) / 255.f;
-  }
-}
-
-// act head output, one workgroup per question: hidden = gelu(sum of partials + a0b) in LDS, then
-// one wave per act output.
-__global__ __launch_bounds__(256) void act_out_kernel(ActOutArgs a) {
-  const int q = blockIdx.x;
-  const int n_q = *a.n_q;  // consulted only before the stores (all b question slots exist)
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  extern __shared__ float hid[];  // [hidden]
-  for (int o = tid; o < a.hidden; o += 256) {
-    const size_t off = static_cast<size_t>(q) * a.hidden + o;
-    // Partials summed in split order, loaded eight at a time (one round trip per group).
-    const float bias = a.a0b[o];
-    float v = 0.f;
-    for (int s0 = 0; s0 < a.splits; s0 += 8) {
-      float t[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) t[u] = a.parts[min(s0 + u, a.splits - 1) * a.split_stride + off];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v = s0 + u < a.splits ? v + t[u] : v;
+  for (int j = count + 1 + tid; j <= a.k; j += kTailThreads) logits[j] = 0.f;
+  __syncthreads();
+  if (wave == 0) {
+    const float* z = zl + 1;
+    float mx = -INFINITY;
+    for (int j = lane; j < count; j += 64) mx = fmaxf(mx, z[j]);
+    mx = wave_max(mx);
+    float se = 0.f;
+    for (int j = lane; j < count; j += 64) se += expf(z[j] - mx);
+    se = wave_sum(se);
+    float ent = 0.f, t1 = 0.f, t2 = 0.f;  // entropy and the two largest probabilities
+    for (int j = lane; j < count; j += 64) {
+      const float p = expf(z[j] - mx) / se;
+      ent -= p * logf(fmaxf(p, 1e-9f));
+      if (p > t1) {
+        t2 = t1;
+        t1 = p;
+      } else {
+        t2 = fmaxf(t2, p);
+      }
     }
-    hid[o] = gelu(v + bias);
+    ent = wave_sum(ent);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      const float o1 = __shfl_xor(t1, d, 64), o2 = __shfl_xor(t2, d, 64);
+      t2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
+      t1 = fmaxf(t1, o1);
+    }
+    if (lane == 0) {
+      const int n = max(count, 2);
+      fv[0] = t1;
+      fv[1] = t1 - t2;
+      fv[2] = ent / logf(static_cast<float>(n));
+      fv[3] = static_cast<float>(n) / 255.f;
+    }
   }
   __syncthreads();
-  for (int o = wave; o < a.n_act; o += 4) {
-    const float* w = a.a2w + static_cast<size_t>(o) * a.hidden;
+  const float f0 = fv[0], f1 = fv[1], f2 = fv[2], f3 = fv[3];
+  auto finish = [&](float v, float4 w, float bias) {  // + the four feature columns, + a0, GELU
+    v = v + w.x * f0;
+    v = v + w.y * f1;
+    v = v + w.z * f2;
+    v = v + w.w * f3;
+    return gelu(v + bias);
+  };
+  if (tid < a.hidden) hid[tid] = finish(pv, pw, pb);
+  for (int o = tid + kTailThreads; o < a.hidden; o += kTailThreads)
+    hid[o] = finish(act_partial(o), *reinterpret_cast<const float4*>(a.a0w + static_cast<size_t>(o) * a.a0_ld + D),
+                    a.a0b[o]);
+  __syncthreads();
+  for (int o = wave; o < a.n_act; o += kTailWaves) {
     float s = 0.f;
-    for (int e = lane; e < a.hidden; e += 64) s += hid[e] * w[e];
+    if (o == wave && a.hidden <= kTailHidden) {
+#pragma unroll
+      for (int j = 0; j < HR; ++j)
+        if (lane + 64 * j < a.hidden) s += hid[lane + 64 * j] * w2[j];
+    } else {
+      const float* w = a.a2w + static_cast<size_t>(o) * a.hidden;
+      for (int e = lane; e < a.hidden; e += 64) s += hid[e] * w[e];
+    }
     s = wave_sum(s);
-    if (lane == 0 && q < n_q) a.acts[static_cast<size_t>(q) * a.n_act + o] = s + a.a2b[o];
+    if (lane == 0) acts[o] = s + a.a2b[o];
   }
 }
 
@@ -326,39 +378,28 @@ int head_gemm_splits(int rows, int N, int K, int cus) {
   return s;
 }
 
-hipError_t launch_head_gemm(const HeadGemmArgs& a, hipStream_t stream) {
+hipError_t launch_head_gemm(const HeadGemmArgs& a, const HeadGemmArgs& b, hipStream_t stream) {
   if (a.cap <= 0) return hipSuccess;
   if (a.N % 64 || a.K % (a.splits * 32)) return hipErrorInvalidValue;
-  const dim3 grid(a.N / 64, (a.cap + 31) / 32, a.splits);
-  LAYA_LAUNCH(head_gemm_kernel, grid, dim3(256), 0, stream, a);
+  if (b.cap > 0 && (b.N % 64 || b.K % (b.splits * 32))) return hipErrorInvalidValue;
+  const HeadGemmPair p{a, b, head_gemm_blocks(a)};
+  const int blocks = p.blocks0 + (b.cap > 0 ? head_gemm_blocks(b) : 0);
+  LAYA_LAUNCH(head_gemm_kernel, dim3(blocks), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
-hipError_t launch_head_logit(const HeadLogitArgs& a, int width, hipStream_t stream) {
-  if (a.cap <= 0) return hipSuccess;
-  const dim3 grid((a.cap + 3) / 4), block(256);
+hipError_t launch_head_tail(const HeadTailArgs& a, int width, hipStream_t stream) {
+  if (a.b <= 0) return hipSuccess;
+  const size_t lds = static_cast<size_t>(a.k + 1 + 4 + a.hidden) * sizeof(float);
+  if (lds > 64 * 1024 || a.a0_ld < width + 4) return hipErrorInvalidValue;
+  const dim3 grid(a.b), block(kTailThreads);
   switch (width) {
-#define LAYA_CASE(D) case D: LAYA_LAUNCH((head_logit_kernel<D>), grid, block, 0, stream, a); break;
+#define LAYA_CASE(D) case D: LAYA_LAUNCH((head_tail_kernel<D>), grid, block, lds, stream, a); break;
     LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
     LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
 #undef LAYA_CASE
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
-}
-
-hipError_t launch_head_features(const HeadFeatureArgs& a, hipStream_t stream) {
-  if (a.b <= 0) return hipSuccess;
-  if (a.kp < a.width + 4) return hipErrorInvalidValue;
-  LAYA_LAUNCH(head_features_kernel, dim3(a.b), dim3(256), 0, stream, a);
-  return hipGetLastError();
-}
-
-hipError_t launch_act_out(const ActOutArgs& a, hipStream_t stream) {
-  if (a.b <= 0) return hipSuccess;
-  const size_t lds = static_cast<size_t>(a.hidden) * sizeof(float);
-  if (lds > 64 * 1024) return hipErrorInvalidValue;
-  LAYA_LAUNCH(act_out_kernel, dim3(a.b), dim3(256), lds, stream, a);
   return hipGetLastError();
 }
 

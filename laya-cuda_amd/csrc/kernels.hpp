@@ -177,59 +177,49 @@ struct GatherRowsArgs {
 hipError_t launch_gather_rows(const GatherRowsArgs& a, int width, DType t, hipStream_t stream);
 
 struct HeadGemmArgs {
-  const float* x;  // [cap][K]
-  const float* w;  // [N][K]
+  const float* x;  // [cap][ldx] (row r of the product is x row x_rows[r] when x_rows is set)
+  const float* w;  // [N][ldw]
   float* parts;    // [splits][cap][N]
   const int32_t* n_rows;  // device scalar (rows actually present)
   int cap, N, K, splits;
   long long split_stride;
+  const int32_t* x_rows = nullptr;  // optional row map into x, clamped to [0, x_cap)
+  int x_cap = 0;
+  int ldx = 0, ldw = 0;  // row strides; 0: K
 };
 int head_gemm_splits(int rows, int N, int K, int cus);
-hipError_t launch_head_gemm(const HeadGemmArgs& a, hipStream_t stream);
+// Two independent products in one launch (the scorer's hidden layer and the act head's CLS-row
+// columns); b.cap == 0 launches the first alone.
+hipError_t launch_head_gemm(const HeadGemmArgs& a, const HeadGemmArgs& b, hipStream_t stream);
 
-// scorer tail per head row: logit = w3 . gelu(sum of scorer.1 partials + b1) + b3
-struct HeadLogitArgs {
+// Head tail, one workgroup per question slot (laya.py:238-245, kernels.cu:167-183):
+//   logit  = w3 . gelu(sum of scorer.1 partials + b1) + b3 for its CLS and option rows;
+//   features: p1, p1-p2, entropy/log(max(n,2)), max(n,2)/255 of the option logits;
+//   hidden = gelu(act_head.0's CLS-row partials + its feature columns . features + a0);
+//   acts   = A2 hidden + a2.
+// Unused question slots of the shape class get zero logits and acts.
+struct HeadTailArgs {
   const float* parts;  // scorer.1 partial products [splits][cap][d]
   int splits;
   long long split_stride;
-  const float* b1;     // scorer.1 bias [d]
-  const float* w3;     // scorer.3 weight [d]
-  const float* b3;     // scorer.3 bias [1]
-  const int32_t* sel_q;   // [cap] question of each compact head row
-  const int32_t* qoff;    // [b] first compact head row of each question
-  const int32_t* n_sel;   // device scalar
-  float* row_logit;  // [cap]
-  float* logits;     // [b][k+1]
-  int cap, k;
-};
-hipError_t launch_head_logit(const HeadLogitArgs& a, int width, hipStream_t stream);
-
-// per question: softmax statistics of its option logits -> act-head input row
-struct HeadFeatureArgs {
-  const float* row_logit;  // [cap]
-  const float* selected;   // [cap][d] gathered rows (CLS row opens each question)
-  const int32_t* counts;   // [b]
-  const int32_t* qoff;     // [b]
-  const int32_t* n_q;      // device scalar
-  float* logits;  // [b][k+1]: unused slots are zeroed here
-  float* feat;    // [b][kp]: CLS row | p1, p1-p2, entropy/log(max(n,2)), max(n,2)/255 | zeros
-  float* acts;    // [b][n_act]: zeroed for unused question slots
-  int b, k, width, kp, n_act;
-};
-hipError_t launch_head_features(const HeadFeatureArgs& a, hipStream_t stream);
-
-// act head output: acts = A2 gelu(sum of act_head.0 partials + a0) + a2
-struct ActOutArgs {
-  const float* parts;  // [splits][b][hidden]
-  int splits;
-  long long split_stride;
+  const float* b1;  // scorer.1 bias [d]
+  const float* w3;  // scorer.3 weight [d]
+  const float* b3;  // scorer.3 bias [1]
+  const float* aparts;  // act_head.0 partial products over the CLS row's d columns [asplits][b][hidden]
+  int asplits;
+  long long asplit_stride;
+  const float* a0w;  // act_head.0 weight [hidden][a0_ld]: columns d..d+3 take the features
+  int a0_ld;
   const float* a0b;  // [hidden]
   const float* a2w;  // [n_act][hidden]
   const float* a2b;  // [n_act]
-  const int32_t* n_q;
-  float* acts;  // [b][n_act]
-  int b, hidden, n_act;
+  const int32_t* counts;  // [b]
+  const int32_t* qoff;    // [b] first compact head row of each question
+  const int32_t* n_q;     // device scalar
+  float* logits;  // [b][k+1]
+  float* acts;    // [b][n_act]
+  int b, k, hidden, n_act;
 };
-hipError_t launch_act_out(const ActOutArgs& a, hipStream_t stream);
+hipError_t launch_head_tail(const HeadTailArgs& a, int width, hipStream_t stream);
 
 }  // namespace laya

@@ -125,7 +125,7 @@ struct Slot {
   void *x = nullptr, *q = nullptr, *kk = nullptr, *vt = nullptr, *attn = nullptr, *ff = nullptr;
   float* part = nullptr;
   float *selected = nullptr, *normed = nullptr, *hpart = nullptr, *logits = nullptr, *acts = nullptr;
-  float *row_logit = nullptr, *feat = nullptr, *apart = nullptr;
+  float* apart = nullptr;
   // Last head transformer layer, on the compact readout rows: attention rows, normalised rows,
   // FFN rows and split-K partials.
   void *attn_sel = nullptr, *x_sel = nullptr, *ff_sel = nullptr;
@@ -179,8 +179,6 @@ struct Engine {
   const float *tok = nullptr, *pos = nullptr, *type0 = nullptr, *emb_g = nullptr, *emb_b = nullptr;
   const float *type_emb = nullptr, *s0w = nullptr, *s0b = nullptr, *s1w = nullptr, *s1b = nullptr;
   const float *s3w = nullptr, *s3b = nullptr, *a0w = nullptr, *a0b = nullptr, *a2w = nullptr, *a2b = nullptr;
-  float* a0w_pad = nullptr;  // act_head.0 weight [act_hidden][act_k], zero columns past d+4
-  int act_k = 0;
   std::list<Slot*> lru;  // front = least recently used
   hipEvent_t static_start = nullptr, static_end = nullptr;  // timing of laya_predict_static
   void* lib = nullptr;  // hipBLASLt handle, created with the first batched slot
@@ -383,7 +381,10 @@ void plan_slot(const Engine& E, Slot* s, int m, int b, int k) {
   const int block = attention_block_rows(s->attn_mode, s->attn_waves);
   s->attn_tiles = std::min(s->L.T, m / block + 2 * b + 1);
   s->head_splits = head_gemm_splits(s->L.R, d, d, E.cus);
-  s->act_splits = head_gemm_splits(b, c.act_hidden, E.act_k, E.cus);
+  // act_head.0's CLS-row columns: at least enough splits that each covers at most 128 columns (one
+  // staged chunk, one memory round trip), so this product ends no later than the scorer's.
+  s->act_splits = head_gemm_splits(b, c.act_hidden, d, E.cus);
+  while (d / s->act_splits > 128 && d % (s->act_splits * 2 * 32) == 0) s->act_splits *= 2;
 }
 
 // The device buffers of a planned slot, in arena order, each starting at a 256-byte boundary.
@@ -414,12 +415,10 @@ size_t carve_slot(const Engine& E, Slot* s, char* base) {
       {reinterpret_cast<void**>(&s->selected), Rz * d * 4},
       {reinterpret_cast<void**>(&s->normed), Rz * d * 4},
       {reinterpret_cast<void**>(&s->hpart), Rz * d * 4 * s->head_splits},
-      {reinterpret_cast<void**>(&s->row_logit), Rz * 4},
       {&s->attn_sel, rows_sel * d * h2},
       {&s->x_sel, rows_sel * d * h2},
       {&s->ff_sel, rows_sel * 4 * d * h2},
       {reinterpret_cast<void**>(&s->part_sel), rows_sel * d * 4 * sel_split},
-      {reinterpret_cast<void**>(&s->feat), static_cast<size_t>(b) * E.act_k * 4},
       {reinterpret_cast<void**>(&s->apart), static_cast<size_t>(b) * c.act_hidden * 4 * s->act_splits},
       {reinterpret_cast<void**>(&s->logits), static_cast<size_t>(b) * (k + 1) * 4},
       {reinterpret_cast<void**>(&s->acts), static_cast<size_t>(b) * c.n_act * 4},
@@ -452,12 +451,12 @@ void check_launch(hipError_t e, const char* what) {
 enum Stage : int {
   kEmbed = 0, kQkv, kAttention, kAttnOut, kAttnNorm, kFfnUp, kFfnDown, kFfnNorm,
   kTypeNorm, kHlQkv, kHlAttention, kHlGather, kHlOut, kHlNorm2, kHlUp, kHlDown, kHlNorm,
-  kHeadGather, kHeadScorer, kHeadLogit, kHeadFeatures, kActHidden, kActOut, kStageCount
+  kHeadGather, kHeadScorer, kHeadTail, kStageCount
 };
 const char* const kStageNames[kStageCount] = {
     "embed_norm", "qkv", "attention", "attn_out", "attn_norm", "ffn_up", "ffn_down", "ffn_norm",
     "type_norm", "head_qkv", "head_attention", "head_gather_rows", "head_out", "head_norm2", "head_up",
-    "head_down", "head_norm", "head_gather", "head_scorer", "head_logit", "head_features", "act_hidden", "act_out"};
+    "head_down", "head_norm", "head_gather", "head_scorer", "head_tail"};
 bool per_layer(int stage) { return stage >= kQkv && stage <= kFfnNorm; }
 bool per_head_layer(int stage) { return stage >= kHlQkv && stage <= kHlNorm; }
 // Whether a stage belongs to this engine's forward (for layer `layer` of its kind).
@@ -682,32 +681,24 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       break;
     }
     case kHeadScorer: {
+      // scorer.1 over the head rows and, in the same launch, act_head.0's CLS-row columns (its
+      // input is the question's CLS row of `selected` and four features the tail adds).
       HeadGemmArgs hm{s.normed, E.s1w, s.hpart, P + L.n_sel, L.R, d, d, s.head_splits, static_cast<long long>(L.R) * d};
-      check_launch(launch_head_gemm(hm, st), "scorer");
-      break;
-    }
-    case kHeadLogit: {
-      HeadLogitArgs hlg{s.hpart, s.head_splits, static_cast<long long>(L.R) * d, E.s1b, E.s3w, E.s3b,
-                        P + L.sel_q, P + L.qoff, P + L.n_sel, s.row_logit, s.logits, L.R, s.k};
-      check_launch(launch_head_logit(hlg, d, st), "head logit");
-      break;
-    }
-    case kHeadFeatures: {
-      HeadFeatureArgs hf{s.row_logit, s.selected, P + L.counts, P + L.qoff, P + L.meta + 1, s.logits, s.feat,
-                         s.acts, s.b, s.k, d, E.act_k, c.n_act};
-      check_launch(launch_head_features(hf, st), "head features");
-      break;
-    }
-    case kActHidden: {
-      HeadGemmArgs ha{s.feat, E.a0w_pad, s.apart, P + L.meta + 1, s.b, c.act_hidden, E.act_k, s.act_splits,
+      HeadGemmArgs ha{s.selected, E.a0w, s.apart, P + L.meta + 1, s.b, c.act_hidden, d, s.act_splits,
                       static_cast<long long>(s.b) * c.act_hidden};
-      check_launch(launch_head_gemm(ha, st), "act hidden");
+      ha.x_rows = P + L.qoff;
+      ha.x_cap = L.R;
+      ha.ldx = d;
+      ha.ldw = d + 4;  // act_head.0.weight rows: the d CLS columns, then the four feature columns
+      check_launch(launch_head_gemm(hm, ha, st), "scorer");
       break;
     }
-    case kActOut: {
-      ActOutArgs ao{s.apart, s.act_splits, static_cast<long long>(s.b) * c.act_hidden, E.a0b, E.a2w, E.a2b,
-                    P + L.meta + 1, s.acts, s.b, c.act_hidden, c.n_act};
-      check_launch(launch_act_out(ao, st), "act out");
+    case kHeadTail: {
+      HeadTailArgs ht{s.hpart, s.head_splits, static_cast<long long>(L.R) * d, E.s1b, E.s3w, E.s3b,
+                      s.apart, s.act_splits, static_cast<long long>(s.b) * c.act_hidden, E.a0w, d + 4,
+                      E.a0b, E.a2w, E.a2b, P + L.counts, P + L.qoff, P + L.meta + 1, s.logits, s.acts,
+                      s.b, s.k, c.act_hidden, c.n_act};
+      check_launch(launch_head_tail(ht, d, st), "head tail");
       break;
     }
     default:
@@ -1069,7 +1060,6 @@ int laya_create(const LayaConfig* cfg, int device, int max_slots, void** handle)
     LAYA_REQUIRE(std::strncmp(prop.gcnArchName, "gfx950", 6) == 0,
                  std::string(prop.name) + " is " + prop.gcnArchName + "; liblaya_hip is built for gfx950 (MI355X)");
     E->cus = prop.multiProcessorCount;
-    E->act_k = (cfg->width + 4 + 255) / 256 * 256;
     E->modern = cfg->norm_order == LAYA_NORM_PRE;
     prepare_device();
     LAYA_HIP(hipStreamCreateWithFlags(&E->stream, hipStreamNonBlocking));
@@ -1202,23 +1192,6 @@ int laya_finalize(void* handle) {
     E->a0b = f32(*E, "act_head.0.bias");
     E->a2w = f32(*E, "act_head.2.weight");
     E->a2b = f32(*E, "act_head.2.bias");
-    {
-      // act_head.0 padded with zero columns to act_k (a multiple of 256): the fp32 MFMA GEMM then
-      // splits K 8-16 ways; the padding multiplies zero features.
-      const int d4 = E->cfg.width + 4, hid = E->cfg.act_hidden;
-      std::vector<float> w(static_cast<size_t>(hid) * d4), padded(static_cast<size_t>(hid) * E->act_k, 0.f);
-      LAYA_HIP(hipMemcpy(w.data(), E->a0w, w.size() * 4, hipMemcpyDeviceToHost));
-      for (int o = 0; o < hid; ++o)
-        std::memcpy(&padded[static_cast<size_t>(o) * E->act_k], &w[static_cast<size_t>(o) * d4], d4 * 4);
-      if (E->a0w_pad) {
-        (void)hipFree(E->a0w_pad);
-        E->a0w_pad = nullptr;
-        E->weight_bytes -= padded.size() * 4;
-      }
-      LAYA_HIP(hipMalloc(reinterpret_cast<void**>(&E->a0w_pad), padded.size() * 4));
-      E->weight_bytes += padded.size() * 4;
-      LAYA_HIP(hipMemcpy(E->a0w_pad, padded.data(), padded.size() * 4, hipMemcpyHostToDevice));
-    }
     // Graphs captured earlier hold old weight pointers: drop every slot.
     for (Slot* s : E->lru) destroy_slot(*E, s);
     E->lru.clear();
@@ -1456,7 +1429,6 @@ int laya_destroy(void* handle) {
   lib_handle_destroy(E->lib);
   for (auto& kv : E->weights) (void)hipFree(kv.second.ptr);
   E->weights.clear();
-  if (E->a0w_pad) (void)hipFree(E->a0w_pad);
   if (E->rope) (void)hipFree(E->rope);
   if (E->static_start) (void)hipEventDestroy(E->static_start);
   if (E->static_end) (void)hipEventDestroy(E->static_end);

@@ -391,7 +391,7 @@ def test_stage_launch_counts_follow_the_variant(gpu):
         assert counts["embed_norm"] == (1, 0) and counts["qkv"] == (3, 0)
         # the last layer's residual + LayerNorm runs inside the head gather, on the gathered rows only
         assert counts["ffn_norm"] == (2, 0)
-        assert counts["head_gather"] == (1, 0) and counts["act_out"] == (1, 0)
+        assert counts["head_gather"] == (1, 0) and counts["head_tail"] == (1, 0) and "act_out" not in counts
         assert counts["type_norm"] == (0, -1) and counts["head_qkv"] == (0, -1)
     finally:
         rt.close()
