@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <list>
 #include <mutex>
@@ -789,8 +790,18 @@ bool captures_as_kernels(Engine& E, Slot& s, int stage) {
 
 // Times the slot's out and down projections as the forward launches them (layer 0, on the slot's
 // own buffers), first with the MFMA tiles, then with each library candidate that runs and
-// captures cleanly, and keeps a candidate only where it is more than 3% faster.
+// captures cleanly, and keeps a candidate only where it is more than 3% faster.  The environment
+// variable LAYA_LIB_GEMMS=off keeps the MFMA tiles, =force takes the first candidate that runs and
+// captures (tests of the library path).
 void choose_lib_gemms(Engine& E, Slot& s) {
+  const char* mode_env = std::getenv("LAYA_LIB_GEMMS");
+  const std::string mode = mode_env ? mode_env : "";
+  if (mode == "off") {
+    for (LibGemm* g : s.lib)
+      if (g) lib_gemm_choose(g, -1);
+    return;
+  }
+  const bool force = mode == "force";
   auto best_of_3 = [&](int stage) {
     float best = 1e30f;
     for (int r = 0; r < 3; ++r) {
@@ -810,7 +821,7 @@ void choose_lib_gemms(Engine& E, Slot& s) {
     const int stage = i ? kFfnDown : kAttnOut;
     lib_gemm_choose(g, -1);
     launch_stage(E, s, stage, 0);  // warm
-    float best = best_of_3(stage) * 0.97f;
+    float best = force ? 1e30f : best_of_3(stage) * 0.97f;
     int pick = -1;
     for (int cand = 0; cand < lib_gemm_candidates(g); ++cand) {
       lib_gemm_choose(g, cand);
@@ -826,6 +837,7 @@ void choose_lib_gemms(Engine& E, Slot& s) {
       if (ms < best) {
         best = ms;
         pick = cand;
+        if (force) break;
       }
     }
     lib_gemm_choose(g, pick);

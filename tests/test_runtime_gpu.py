@@ -135,6 +135,34 @@ def test_batched_encoder_matches_oracle(gpu, dtype):
         rt.close()
 
 
+@pytest.mark.parametrize("mode", ["force", "off"])
+def test_library_projections_match_oracle(gpu, mode, monkeypatch):
+    """A BERT-style batched slot past 12,288 packed rows with the library path forced
+    (LAYA_LIB_GEMMS=force: the out and down projections, bias included, on hipBLASLt's kernels)
+    and switched off (every projection on the MFMA tiles): fp16 logits within 1e-3 of the oracle
+    either way, and the graph replay equal to the eager forward bit for bit."""
+    monkeypatch.setenv("LAYA_LIB_GEMMS", mode)
+    spec = synthetic.adapter(None, layers=2, width=256, heads=4, intermediate=1024, vocab=3000, positions=1024,
+                             max_len=1024)
+    w = synthetic.weights(spec, seed=23)
+    rng = np.random.default_rng(24)
+    lengths = rng.integers(700, 1000, 16)
+    sequences = [rng.integers(5, 3000, int(n), dtype=np.int32) for n in lengths]
+    questions = [(i, sorted(rng.choice(np.arange(1, int(n)), 4, replace=False).tolist()), i % 3)
+                 for i, n in enumerate(lengths)]
+    want, want_acts = oracle_logits(spec, w, sequences, questions)
+    rt = Runtime(spec, 0, 1, weights=w)
+    try:
+        logits, acts, metrics = rt.predict_sequences(sequences, questions)
+        assert metrics["shape"][0] >= 12288 and metrics["graph_replay"], metrics["shape"]
+        eager = rt.predict_sequences(sequences, questions, capture=False)
+        np.testing.assert_array_equal(eager[0], logits)
+        np.testing.assert_array_equal(eager[1], acts)
+        compare(logits, acts, want, want_acts, label=f"library projections {mode} rows {metrics['shape'][0]}")
+    finally:
+        rt.close()
+
+
 def test_reference_items_each_question_its_own_row(gpu):
     """Runtime.predict(items) packs every question as its own sequence (runtime.py:52-68)."""
     spec = synthetic.adapter(None, layers=2, width=128, heads=2, intermediate=512, vocab=1000, positions=64,
