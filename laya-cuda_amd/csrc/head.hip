@@ -388,10 +388,25 @@ hipError_t launch_head_gemm(const HeadGemmArgs& a, const HeadGemmArgs& b, hipStr
   return hipGetLastError();
 }
 
+// The tail's LDS (logits, features, act hidden) can pass the default 64 KB for wide act heads or
+// large option capacities: allow the whole 160 KB of a gfx950 CU, once per device.
+constexpr size_t kTailMaxLds = 160 * 1024;
+hipError_t head_prepare() {
+  hipError_t e = hipSuccess;
+#define LAYA_CASE(D)                                                                                     \
+  if (e == hipSuccess)                                                                                   \
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(&head_tail_kernel<D>),                         \
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kTailMaxLds));
+  LAYA_CASE(64) LAYA_CASE(128) LAYA_CASE(256) LAYA_CASE(384) LAYA_CASE(512) LAYA_CASE(768)
+  LAYA_CASE(1024) LAYA_CASE(1088) LAYA_CASE(1280) LAYA_CASE(1536) LAYA_CASE(2048)
+#undef LAYA_CASE
+  return e;
+}
+
 hipError_t launch_head_tail(const HeadTailArgs& a, int width, hipStream_t stream) {
   if (a.b <= 0) return hipSuccess;
   const size_t lds = static_cast<size_t>(a.k + 1 + 4 + a.hidden) * sizeof(float);
-  if (lds > 64 * 1024 || a.a0_ld < width + 4) return hipErrorInvalidValue;
+  if (lds > kTailMaxLds || a.a0_ld < width + 4) return hipErrorInvalidValue;
   const dim3 grid(a.b), block(kTailThreads);
   switch (width) {
 #define LAYA_CASE(D) case D: LAYA_LAUNCH((head_tail_kernel<D>), grid, block, lds, stream, a); break;

@@ -221,5 +221,7 @@ struct HeadTailArgs {
   int b, k, hidden, n_act;
 };
 hipError_t launch_head_tail(const HeadTailArgs& a, int width, hipStream_t stream);
+// Once per device before the first tail launch: the tail kernels' dynamic LDS limit.
+hipError_t head_prepare();
 
 }  // namespace laya

@@ -972,7 +972,8 @@ std::vector<int> g_prepared;
 // Per device: the device address of `scratch` (each device holds its own copy of the array).
 constexpr int kMaxDevices = 64;
 void* g_scratch[kMaxDevices] = {};
-// One-time set-up of the current device: GEMM kernel attributes and the scratch address.
+// One-time set-up of the current device: GEMM and head-tail kernel attributes and the scratch
+// address.
 void prepare_device() {
   int dev = 0;
   LAYA_HIP(hipGetDevice(&dev));
@@ -981,6 +982,7 @@ void prepare_device() {
     if (d == dev) return;
   LAYA_REQUIRE(dev >= 0 && dev < kMaxDevices, "device index beyond the library's device table");
   LAYA_HIP(gemm_prepare());
+  LAYA_HIP(head_prepare());
   void* ptr = nullptr;
   LAYA_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
   LAYA_REQUIRE(ptr != nullptr, "no device address for the scratch array");

@@ -163,6 +163,28 @@ def test_library_projections_match_oracle(gpu, mode, monkeypatch):
         rt.close()
 
 
+@pytest.mark.parametrize("hidden", [1024, 16384])
+def test_wide_act_head_matches_oracle(gpu, hidden):
+    """Act heads wider than the reference's 256 (the C ABI takes any multiple of 64 up to 16,384):
+    the head tail's outputs past its 512 threads and its unprefetched act_head.2 rows (1,024), and
+    a tail LDS past the default 64 KB (16,384 hidden values plus the logits), against the oracle."""
+    spec = synthetic.adapter(None, layers=2, width=64, heads=1, intermediate=256, vocab=500, positions=128,
+                             max_len=128)
+    spec.act_hidden = hidden
+    w = synthetic.weights(spec, seed=29)
+    rng = np.random.default_rng(30)
+    lengths = [70, 33]
+    sequences = [rng.integers(5, 500, n, dtype=np.int32) for n in lengths]
+    questions = [(0, [3, 9, 20, 41, 60], 0), (1, [2, 30], 2), (0, [7], 1)]
+    want, want_acts = oracle_logits(spec, w, sequences, questions)
+    rt = Runtime(spec, 0, 1, weights=w)
+    try:
+        logits, acts, _ = rt.predict_sequences(sequences, questions)
+        compare(logits, acts, want, want_acts, label=f"act head {hidden}")
+    finally:
+        rt.close()
+
+
 def test_reference_items_each_question_its_own_row(gpu):
     """Runtime.predict(items) packs every question as its own sequence (runtime.py:52-68)."""
     spec = synthetic.adapter(None, layers=2, width=128, heads=2, intermediate=512, vocab=1000, positions=64,
