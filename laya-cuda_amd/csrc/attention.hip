@@ -43,6 +43,17 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
   asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
   return r;
 }
+// The same for the first instruction that reads an MFMA's result registers: a VALU read of an
+// MFMA destination needs wait states after the MFMA (the pass count plus a few for the 8-pass
+// 32x32x16 MFMAs here) that the compiler inserts for its own instructions but not in front of inline
+// assembly, so this one carries 16 of them itself; every later read of those registers depends on
+// its result.  (Without them, a half-block variant whose first read came right after its MFMA
+// gave results that differed from run to run.)
+__device__ __forceinline__ float max3_after_mfma(float a, float b, float c) {
+  float r;
+  asm("s_nop 7\n\ts_nop 7\n\tv_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
 
 // Combine a value with the one held by lane l ^ 32 (the other half of the S^T accumulator's k-slots
 // for the same query) with v_permlane32_swap: a VALU lane exchange, no LDS round trip.
@@ -102,14 +113,15 @@ __device__ __forceinline__ void softmax_block(f32x16 (&s)[2], f32x16 (&o)[2], fl
         s[kt][r] = out ? -INFINITY : s[kt][r];
       }
   }
-  // Block maximum of the lane's 32 scores: two chains of v_max3 (16 instructions).
-  float mx[2] = {max3(s[0][0], s[0][1], s[0][2]), max3(s[1][0], s[1][1], s[1][2])};
+  // Block maximum of the lane's 32 scores: two chains of v_max3 (16 instructions), each opened by
+  // the instruction that waits for its MFMA results; s[1][15] is read only after its chain's opener.
+  float mx[2] = {max3_after_mfma(s[0][0], s[0][1], s[0][2]), max3_after_mfma(s[1][0], s[1][1], s[1][2])};
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int r = 3; r < 15; r += 2) mx[kt] = max3(mx[kt], s[kt][r], s[kt][r + 1]);
-  float bmax = max3(mx[0], s[0][15], s[1][15]);
-  bmax = max3(bmax, mx[1], mx[1]);
+  float bmax = max3(mx[0], mx[1], s[0][15]);
+  bmax = max3(bmax, s[1][15], s[1][15]);
   bmax = half_max(bmax) * c;
   const bool grow = bmax > mrow + kSlack;  // false while everything seen so far is masked
   if (__builtin_amdgcn_ballot_w64(grow)) {
