@@ -230,27 +230,28 @@ class Laya(EncoderSpec):
     def encode(self, value):
         return self.tokenizer.encode(value.replace(self.mask_text, " "), add_special_tokens=False).ids
 
-    def state_ids(self, text):
+    def state_ids(self, text, need=None):
         """The state text's ids as far as prepare can use them: the whole text's, or at least their
-        first max_len.  The reference encodes the whole state and keeps its first max_len - 3 or
-        fewer ids (laya.py:110-130), so a long state costs the tokenizer time for every character.
-        Where the tokenizer splits in front of a space that follows a letter or digit
-        (``prefix_cut``), the text is encoded in pieces cut at such spaces, the first about 6 x
-        max_len characters, each next one sized for the ids still missing, until max_len ids are
-        there: the pieces' ids joined are the whole text's, and the work never exceeds encoding
-        the whole text."""
+        first ``need`` (default max_len).  The reference encodes the whole state and keeps its first
+        max_len - 3 or fewer ids (laya.py:110-130), so a long state costs the tokenizer time for
+        every character.  Where the tokenizer splits in front of a space that follows a letter or
+        digit (``prefix_cut``), the text is encoded in pieces cut at such spaces, the first about
+        5 x ``need`` characters, each next one sized for the ids still missing, until ``need`` ids
+        are there: the pieces' ids joined are the whole text's, and the work never exceeds
+        encoding the whole text."""
         encode = self.tokenizer.encode
         if not self.prefix_cut:
             return encode(text, add_special_tokens=False).ids
-        ids, start, chars = [], 0, 6 * self.max_len
-        while start < len(text) and len(ids) < self.max_len:
+        need = self.max_len if need is None else need
+        ids, start, chars = [], 0, 5 * need + 64
+        while start < len(text) and len(ids) < need:
             end = text.find(" ", start + chars)
             while end > 0 and not text[end - 1].isalnum():
                 end = text.find(" ", end + 1)
             end = end if end > 0 else len(text)
             ids += encode(text[start:end], add_special_tokens=False).ids
             start = end
-            chars = (self.max_len - len(ids)) * start // max(len(ids), 1) * 5 // 4 + 64
+            chars = (need - len(ids)) * start // max(len(ids), 1) * 5 // 4 + 64
         return ids
 
     def prepare(self, state, questions):
@@ -265,12 +266,11 @@ class Laya(EncoderSpec):
             texts.append(f"{kind} question: {instruction}")
             texts.extend(" " + option for option in options)
         texts = [t.replace(self.mask_text, " ") for t in texts]
-        state_ids = self.state_ids(texts[0])
         if len(texts) >= 12:
             encoded = [e.ids for e in self.tokenizer.encode_batch(texts[1:], add_special_tokens=False)]
         else:
             encoded = [self.tokenizer.encode(t, add_special_tokens=False).ids for t in texts[1:]]
-        cursor, items = iter(encoded), []
+        cursor, layouts = iter(encoded), []
         for qid, (kind, _, _, options) in zip(questions, parsed):
             head = next(cursor)
             opts = [[self.mask] + next(cursor)[:48] for _ in options]
@@ -285,7 +285,12 @@ class Laya(EncoderSpec):
                 markers.append(len(ids))
                 ids.extend(opt)
             ids.append(self.sep)
-            room = max(0, self.max_len - len(ids) - 1)
+            layouts.append((qid, kind, ids, markers))
+        # The state's ids after every question's layout: only as many as the roomiest one takes.
+        rooms = [max(0, self.max_len - len(ids) - 1) for _, _, ids, _ in layouts]
+        state_ids = self.state_ids(texts[0], max(rooms))
+        items = []
+        for (qid, kind, ids, markers), room in zip(layouts, rooms):
             ids = (ids + state_ids[:room] + [self.sep])[:self.max_len]
             if markers[-1] >= len(ids):
                 raise ValueError(f"Question {qid!r} exceeds the option token budget")
