@@ -57,3 +57,19 @@ def test_vectors_exercise_the_piecewise_state_encoding(adapters):
     assert laya.prefix_cut
     long = [c for c in VECTORS["cases"] if c["name"] == "long state"]
     assert long and all(len(c["state"]) > 6 * c["max_len"] for c in long)
+
+
+def test_fingerprint_is_sha256_of_compact_json(adapters):
+    """input_sha256 (laya.py:192-193): sha256 of json.dumps(items, separators=(",", ":")), for the
+    prepared items of every golden case and for random items."""
+    import hashlib
+    import random
+    laya = adapters[(512, 160)]
+    rng = random.Random(5)
+    samples = [[(c["items"][0][0], c["items"][0][1], c["items"][0][2])] for c in VECTORS["cases"] if "items" in c]
+    samples += [[([rng.randrange(0, 50000) for _ in range(rng.randrange(1, 600))],
+                  sorted(rng.sample(range(1, 600), rng.randrange(1, 9))), rng.randrange(3))
+                 for _ in range(rng.randrange(1, 5))] for _ in range(50)]
+    for items in samples:
+        want = hashlib.sha256(json.dumps(items, separators=(",", ":")).encode()).hexdigest()
+        assert laya.fingerprint(items) == want
