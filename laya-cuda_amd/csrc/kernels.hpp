@@ -88,23 +88,6 @@ void gemm_plan(int M, int N, int K, Epi epi, DType t, int cus, int* tile, int* s
 hipError_t gemm_prepare();  // sets LDS attributes of the large-tile kernels (call once per device)
 hipError_t launch_gemm(const GemmArgs& a, Epi epi, DType t, int tile, hipStream_t stream);
 
-// ---- plain projections through hipBLASLt (libgemm.hip) ----
-// out[M][N] = x[M][K] W[N][K]^T (+ fp32 bias before the rounding), 16-bit x, W and out: the
-// library's kernel candidates for one problem; the runtime times them against launch_gemm's HALF
-// epilogue and keeps the faster (lib_gemm_choose; -1 keeps launch_gemm).
-constexpr int kLibCandidates = 4;
-struct LibGemm;
-void* lib_handle_create();  // null when the library cannot be set up: launch_gemm is used
-void lib_handle_destroy(void* handle);
-LibGemm* lib_gemm_plan(void* handle, DType t, int M, int N, int K, bool bias, size_t max_ws);  // null: none
-void lib_gemm_destroy(LibGemm* g);
-int lib_gemm_candidates(const LibGemm* g);
-size_t lib_gemm_workspace(const LibGemm* g, int candidate);
-int lib_gemm_chosen(const LibGemm* g);
-void lib_gemm_choose(LibGemm* g, int candidate);
-bool lib_gemm_run(void* handle, LibGemm* g, int candidate, const void* w, const void* x, const float* bias,
-                  void* out, void* ws, hipStream_t stream);
-
 // ---- fused bidirectional attention over packed rows ----
 // tiles: [max_tiles][3] = (row0, row1, seq); seq < 0 marks rows to zero.
 // Attention work list entry (16-byte aligned int4): query rows [row0, row1) of one sequence whose

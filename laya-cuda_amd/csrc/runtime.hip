@@ -12,7 +12,6 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
-#include <cstdlib>
 #include <cstring>
 #include <list>
 #include <mutex>
@@ -140,11 +139,6 @@ struct Slot {
   // linear1, linear2 over the readout rows.
   int htile[7] = {0, 0, 0, 0, 0, 0, 0}, hsplits[7] = {1, 1, 1, 1, 1, 1, 1};
   int attn_mode = 0, attn_waves = 2, attn_tiles = 0, head_splits = 1, act_splits = 1;
-  // Batched slots: the out and down projections through hipBLASLt where its kernel timed faster
-  // on this slot (lib_gemm_chosen >= 0), with their workspace at the end of the arena.
-  LibGemm* lib[2] = {nullptr, nullptr};
-  void* lib_ws = nullptr;
-  size_t lib_ws_bytes = 0;
   hipGraphExec_t graph = nullptr;
   hipEvent_t start = nullptr, end = nullptr;
 };
@@ -182,8 +176,6 @@ struct Engine {
   const float *s3w = nullptr, *s3b = nullptr, *a0w = nullptr, *a0b = nullptr, *a2w = nullptr, *a2b = nullptr;
   std::list<Slot*> lru;  // front = least recently used
   hipEvent_t static_start = nullptr, static_end = nullptr;  // timing of laya_predict_static
-  void* lib = nullptr;  // hipBLASLt handle, created with the first batched slot
-  bool lib_failed = false;
   std::string error;
 
   DType mfma() const { return cfg.mfma_dtype == LAYA_F16 ? DType::F16 : DType::BF16; }
@@ -301,7 +293,6 @@ const DevTensor& need(Engine& E, const std::string& name) {
 const float* f32(Engine& E, const std::string& name) { return static_cast<const float*>(need(E, name).ptr); }
 
 void destroy_slot(Engine& E, Slot* s) {
-  for (LibGemm* g : s->lib) lib_gemm_destroy(g);
   if (s->graph) (void)hipGraphExecDestroy(s->graph);
   if (s->start) (void)hipEventDestroy(s->start);
   if (s->end) (void)hipEventDestroy(s->end);
@@ -423,7 +414,6 @@ size_t carve_slot(const Engine& E, Slot* s, char* base) {
       {reinterpret_cast<void**>(&s->apart), static_cast<size_t>(b) * c.act_hidden * 4 * s->act_splits},
       {reinterpret_cast<void**>(&s->logits), static_cast<size_t>(b) * (k + 1) * 4},
       {reinterpret_cast<void**>(&s->acts), static_cast<size_t>(b) * c.n_act * 4},
-      {&s->lib_ws, s->lib_ws_bytes},
   };
   size_t at = 0;
   for (const Part& p : parts) {
@@ -485,18 +475,6 @@ void use_branch16(const Slot& s, AddNormArgs& na) {
   na.bias = nullptr;
 }
 
-// A batched slot's out (i = 0) or down (i = 1) projection through its chosen hipBLASLt kernel, into
-// the slot's 16-bit branch rows.  Under in-forward stage timing the library's launches are
-// bracketed by the event pair itself (hipEventRecord: the interval also holds the two event packets).
-void run_lib_gemm(Engine& E, Slot& s, int i, const void* w, const void* x, const float* bias, hipStream_t st) {
-  const LaunchTiming timing = launch_timing;
-  launch_timing = LaunchTiming{};
-  if (timing.start) LAYA_HIP(hipEventRecord(timing.start, st));
-  if (!lib_gemm_run(E.lib, s.lib[i], lib_gemm_chosen(s.lib[i]), w, x, bias, s.part, s.lib_ws, st))
-    throw Failure{LAYA_EDEVICE, "hipBLASLt matmul failed"};
-  if (timing.start) LAYA_HIP(hipEventRecord(timing.stop, st));
-}
-
 void launch_stage(Engine& E, Slot& s, int stage, int layer) {
   const LayaConfig& c = E.cfg;
   const int m = s.m, d = c.width, f = c.intermediate, R = s.L.R;
@@ -536,10 +514,6 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       break;
     }
     case kAttnOut:
-      if (s.branch16 && lib_gemm_chosen(s.lib[0]) >= 0) {
-        run_lib_gemm(E, s, 0, ly->wo, s.attn, ly->bo, st);
-        break;
-      }
       g.a = s.attn; g.b = ly->wo; g.M = m; g.N = d; g.K = d; g.lda = d; g.ldb = d;
       g.out = s.part; g.ldo = d; g.split_stride = md; g.splits = s.splits[1];
       if (s.branch16) g.bias = ly->bo;  // null for ModernBERT
@@ -562,10 +536,6 @@ void launch_stage(Engine& E, Slot& s, int stage, int layer) {
       check_launch(launch_gemm(g, E.modern ? Epi::GEGLU : Epi::GELU, t, s.tile[2], st), "ffn up");
       break;
     case kFfnDown:
-      if (s.branch16 && lib_gemm_chosen(s.lib[1]) >= 0) {
-        run_lib_gemm(E, s, 1, ly->wo2, s.ff, ly->bo2, st);
-        break;
-      }
       g.a = s.ff; g.b = ly->wo2; g.M = m; g.N = d; g.K = f; g.lda = f; g.ldb = f;
       g.out = s.part; g.ldo = d; g.split_stride = md; g.splits = s.splits[3];
       if (s.branch16) g.bias = ly->bo2;  // null for ModernBERT
@@ -739,120 +709,10 @@ void forward(Engine& E, Slot& s, int marked = -1, hipEvent_t* marks = nullptr) {
   for (int stage = kHeadScorer; stage < kStageCount; ++stage) run(stage, 0);
 }
 
-// Batched slots of kLibRows or more packed rows: hipBLASLt's kernel candidates for the out and down
-// projections (plain GEMMs with the bias before the rounding), and the workspace the largest needs.
-// Choosing among them costs the slot's creation 1-3 s (the library's handle and kernel code load
-// on first use, then the timing), which large offline batches pay once; smaller batched slots,
-// such as the packs a BatchEngine creates while serving (max_batch_tokens 4,096 by default), keep
-// the MFMA tiles.
-constexpr size_t kLibWorkspace = size_t(32) << 20;
-constexpr int kLibRows = 12288;
-
-void plan_lib_gemms(Engine& E, Slot& s) {
-  if (!E.lib && !E.lib_failed) {
-    E.lib = lib_handle_create();
-    E.lib_failed = E.lib == nullptr;
-  }
-  if (!E.lib) return;
-  const int d = E.cfg.width, f = E.cfg.intermediate;
-  s.lib[0] = lib_gemm_plan(E.lib, E.mfma(), s.m, d, d, E.cfg.bias != 0, kLibWorkspace);
-  s.lib[1] = lib_gemm_plan(E.lib, E.mfma(), s.m, d, f, E.cfg.bias != 0, kLibWorkspace);
-  for (const LibGemm* g : s.lib)
-    for (int cand = 0; cand < lib_gemm_candidates(g); ++cand)
-      s.lib_ws_bytes = std::max(s.lib_ws_bytes, lib_gemm_workspace(g, cand));
-}
-
-// True when `stage` (layer 0) records only kernel nodes into a graph: a candidate whose capture
-// fails, or holds memset or copy nodes, stays out of the forward's graph (memset nodes have given
-// wrong results on replays after the first).
-bool captures_as_kernels(Engine& E, Slot& s, int stage) {
-  if (hipStreamBeginCapture(E.stream, hipStreamCaptureModeThreadLocal) != hipSuccess) return false;
-  bool ok = true;
-  try {
-    launch_stage(E, s, stage, 0);
-  } catch (...) {
-    ok = false;
-  }
-  hipGraph_t graph = nullptr;
-  ok = hipStreamEndCapture(E.stream, &graph) == hipSuccess && ok && graph;
-  size_t n = 0;
-  ok = ok && hipGraphGetNodes(graph, nullptr, &n) == hipSuccess && n > 0;
-  std::vector<hipGraphNode_t> nodes(ok ? n : 0);
-  ok = ok && hipGraphGetNodes(graph, nodes.data(), &n) == hipSuccess;
-  for (size_t j = 0; ok && j < n; ++j) {
-    hipGraphNodeType type;
-    ok = hipGraphNodeGetType(nodes[j], &type) == hipSuccess && type == hipGraphNodeTypeKernel;
-  }
-  if (graph) (void)hipGraphDestroy(graph);
-  (void)hipGetLastError();  // a refused capture leaves no error for the next call
-  return ok;
-}
-
-// Times the slot's out and down projections as the forward launches them (layer 0, on the slot's
-// own buffers), first with the MFMA tiles, then with each library candidate that runs and
-// captures cleanly, and keeps a candidate only where it is more than 3% faster.  The environment
-// variable LAYA_LIB_GEMMS=off keeps the MFMA tiles, =force takes the first candidate that runs and
-// captures (tests of the library path).
-void choose_lib_gemms(Engine& E, Slot& s) {
-  const char* mode_env = std::getenv("LAYA_LIB_GEMMS");
-  const std::string mode = mode_env ? mode_env : "";
-  if (mode == "off") {
-    for (LibGemm* g : s.lib)
-      if (g) lib_gemm_choose(g, -1);
-    return;
-  }
-  const bool force = mode == "force";
-  // Fastest of five launches after two untimed ones (the first launches of a library kernel also
-  // load its code; with three timed launches and one warm-up the choice flipped between processes).
-  auto best_of_5 = [&](int stage) {
-    launch_stage(E, s, stage, 0);
-    launch_stage(E, s, stage, 0);
-    float best = 1e30f;
-    for (int r = 0; r < 5; ++r) {
-      LAYA_HIP(hipEventRecord(s.start, E.stream));
-      launch_stage(E, s, stage, 0);
-      LAYA_HIP(hipEventRecord(s.end, E.stream));
-      LAYA_HIP(hipEventSynchronize(s.end));
-      float ms = 0.f;
-      LAYA_HIP(hipEventElapsedTime(&ms, s.start, s.end));
-      best = std::min(best, ms);
-    }
-    return best;
-  };
-  for (int i = 0; i < 2; ++i) {
-    LibGemm* g = s.lib[i];
-    if (!g) continue;
-    const int stage = i ? kFfnDown : kAttnOut;
-    lib_gemm_choose(g, -1);
-    launch_stage(E, s, stage, 0);  // warm
-    float best = force ? 1e30f : best_of_5(stage) * 0.97f;
-    int pick = -1;
-    for (int cand = 0; cand < lib_gemm_candidates(g); ++cand) {
-      lib_gemm_choose(g, cand);
-      try {
-        launch_stage(E, s, stage, 0);  // loads the candidate's code before the capture check
-        LAYA_HIP(hipStreamSynchronize(E.stream));
-      } catch (const Failure&) {
-        (void)hipGetLastError();
-        continue;
-      }
-      if (!captures_as_kernels(E, s, stage)) continue;
-      const float ms = best_of_5(stage);
-      if (ms < best) {
-        best = ms;
-        pick = cand;
-        if (force) break;
-      }
-    }
-    lib_gemm_choose(g, pick);
-  }
-}
-
 Slot* create_slot(Engine& E, int m, int b, int k) {
   Slot* s = new Slot();
   try {
     plan_slot(E, s, m, b, k);
-    if (s->branch16 && m >= kLibRows) plan_lib_gemms(E, *s);
     const size_t total = carve_slot(E, s, nullptr);
     LAYA_HIP(hipMalloc(&s->arena, total));
     s->bytes = total;
@@ -863,7 +723,6 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
     LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_acts), static_cast<size_t>(b) * E.cfg.n_act * 4, hipHostMallocDefault));
     LAYA_HIP(hipEventCreate(&s->start));
     LAYA_HIP(hipEventCreate(&s->end));
-    if (s->lib[0] || s->lib[1]) choose_lib_gemms(E, *s);
   } catch (...) {
     destroy_slot(E, s);
     throw;
@@ -1444,7 +1303,6 @@ int laya_destroy(void* handle) {
   if (E->stream) (void)hipStreamSynchronize(E->stream);
   for (Slot* s : E->lru) destroy_slot(*E, s);
   E->lru.clear();
-  lib_handle_destroy(E->lib);
   for (auto& kv : E->weights) (void)hipFree(kv.second.ptr);
   E->weights.clear();
   if (E->rope) (void)hipFree(E->rope);

@@ -31,6 +31,17 @@ def test_library_exports_every_declared_symbol():
     assert lib.laya_abi_version() == _lib.ABI_VERSION == 2
 
 
+def test_library_links_no_gemm_library():
+    """Every projection runs on this library's own MFMA kernels: no BLAS library is linked into
+    liblaya_hip.so or referenced by its dynamic symbol table."""
+    import subprocess
+    path = Path(_lib.__file__).resolve().parent / "liblaya_hip.so"
+    symbols = subprocess.run(["nm", "-D", str(path)], check=True, capture_output=True, text=True).stdout
+    needed = subprocess.run(["readelf", "-d", str(path)], check=True, capture_output=True, text=True).stdout
+    for text in (symbols, needed):
+        assert not re.search(r"hipblas|rocblas|cublas", text, re.I)
+
+
 def test_binding_refuses_a_library_of_another_abi_version(monkeypatch):
     monkeypatch.setattr(_lib, "_lib", None)  # force a fresh load
     monkeypatch.setattr(_lib, "ABI_VERSION", _lib.ABI_VERSION + 1)
