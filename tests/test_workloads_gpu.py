@@ -4,10 +4,11 @@
   of 1,024 Zipf(1.1) token ids, three 5-option questions; fp16 operands, logits within 1e-3 and
   identical decisions; embedding rows gathered from the whole table (its last rows included)
   bit for bit.
-* b64x1024: 24L/1024 encoder, 16 heads, FFN 4096, bf16 weights and operands, 64 x 1,024 dense
-  tokens, one 8-option question per sequence.  The whole batch runs on the GPU; sequences are
+* b64x1024: 24L/1024 encoder, 16 heads, FFN 4096, bf16-valued weights, 64 x 1,024 dense tokens,
+  one 8-option question per sequence.  The whole batch runs on the GPU; sequences are
   independent, so three of them (first, middle, last in the packed block) are checked against
   the oracle run on those sequences alone.  Graph replay equals the eager pass bit for bit.
+  fp16 operands (the benchmarked mode) are held to the 1e-3 bound; bf16 operands to 4e-3.
 """
 import ctypes as ct
 
@@ -20,11 +21,16 @@ from test_runtime_gpu import compare, oracle_logits
 
 pytestmark = pytest.mark.gpu
 
-# bf16 operands on the 24-layer d=1024 batch.  The weights are bf16 values by definition, so no
-# weight rounding enters; the bound covers the bf16 rounding of the normalised GEMM inputs,
-# Q/K/V, the attention probabilities and output, the FFN activations and the out/down projection
-# rows added to the fp32 residual (the reference's 16-bit branch).
-B64_LOGIT_ATOL = 4e-3
+# The 24-layer d=1024 batch.  Its weights are bf16 values by definition; fp16 holds every one of them
+# exactly down to 2^-17 (N(0, 0.02) draws below that are rounded by less than 2^-25), so fp16
+# operands add no weight rounding either.  A CPU emulation of this path's rounding points
+# (tests/rounding_emulation.py: 16-bit normalised GEMM inputs, Q/K/V, attention probabilities and
+# output, FFN activations, and the 16-bit out/down projection rows added to the fp32 residual)
+# gives a max logit error on sequences 0, 37 and 63 of 2.78e-4 with fp16 operands and 2.85e-3 with
+# bf16: bf16 cannot meet the 1e-3 bound on this model, fp16 meets it with room.
+B64_LOGIT_ATOL = {"float16": 1e-3, "bfloat16": 4e-3}
+B64_PICKS = [0, 37, 63]
+_b64_oracle = {}
 
 
 def test_l1024_large_vocab_matches_oracle(gpu):
@@ -62,8 +68,9 @@ def test_l1024_large_vocab_matches_oracle(gpu):
     np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), host[pick].view(np.uint32))
 
 
-def test_b64x1024_batch_matches_oracle_on_sampled_sequences(gpu):
-    spec = synthetic.adapter("b64x1024", mfma_dtype="bfloat16")
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_b64x1024_batch_matches_oracle_on_sampled_sequences(gpu, dtype):
+    spec = synthetic.adapter("b64x1024", mfma_dtype=dtype)
     w = synthetic.weights(spec, seed=0, bf16=True)
     sequences, questions = synthetic.request("b64x1024", seed=1)
     assert len(sequences) == 64 and all(len(s) == 1024 for s in sequences)
@@ -77,8 +84,10 @@ def test_b64x1024_batch_matches_oracle_on_sampled_sequences(gpu):
         np.testing.assert_array_equal(eager[1], acts)
     finally:
         rt.close()
-    picks = [0, 37, 63]
-    sub_seqs = [sequences[i] for i in picks]
-    sub_qs = [(j, questions[i][1], questions[i][2]) for j, i in enumerate(picks)]
-    want, want_acts = oracle_logits(spec, w, sub_seqs, sub_qs)
-    compare(logits[picks], acts[picks], want, want_acts, atol=B64_LOGIT_ATOL, label="b64x1024 bf16 (sequences 0, 37, 63)")
+    if not _b64_oracle:  # the oracle does not depend on the operand type: computed once
+        sub_seqs = [sequences[i] for i in B64_PICKS]
+        sub_qs = [(j, questions[i][1], questions[i][2]) for j, i in enumerate(B64_PICKS)]
+        _b64_oracle["want"] = oracle_logits(spec, w, sub_seqs, sub_qs)
+    want, want_acts = _b64_oracle["want"]
+    compare(logits[B64_PICKS], acts[B64_PICKS], want, want_acts, atol=B64_LOGIT_ATOL[dtype],
+            label=f"b64x1024 {dtype} (sequences 0, 37, 63)")
