@@ -40,7 +40,7 @@ def test_identical_answers_pass_every_gate():
 
 def test_decisions_follow_the_answer_type():
     assert gates.decision(choice([0.2, 0.7, 0.1])) == "k1"
-    assert gates.decision(noul(0.5)) is True and gates.decision(noul(0.4999)) is False
+    assert gates.decision(noul(0.5)) == "true" and gates.decision(noul(0.4999)) == "false"
     assert gates.decision(score([0.1, 0.3, 0.6])) == "2"
     assert gates.probability_vector(noul(0.25)) == [0.75, 0.25]
 
@@ -93,3 +93,45 @@ def test_misaligned_or_non_finite_inputs():
     cand[0]["answers"]["q1"]["noul"] = float("nan")
     assert gates.failures(gates.agreement(cand, REFERENCE)) == ["non-finite probabilities"]
     assert gates.failures(gates.agreement([], [])) == ["no decisions"]
+
+
+@pytest.mark.parametrize("wins,losses,p", [
+    (0, 0, 1.0),          # nothing decided differently
+    (3, 0, 1.0),          # no losses: every outcome has at least 0
+    (0, 1, 0.5),          # C(1,1)/2
+    (0, 4, 1 / 16),       # C(4,4)/16
+    (0, 5, 1 / 32),       # 0.03125 < 0.05
+    (1, 4, 6 / 32),       # (C(5,4) + C(5,5))/32
+    (2, 7, 46 / 512),     # (36 + 9 + 1)/512
+    (5, 5, 638 / 1024),   # sum_{k>=5} C(10,k)/1024
+])
+def test_sign_test_p_values(wins, losses, p):
+    assert math.isclose(gates.sign_test(wins, losses), p, rel_tol=1e-12)
+
+
+def test_accuracy_gate_uses_gold_labels():
+    """Candidate and reference disagree only where a gold label exists: five questions the
+    reference gets right and the candidate wrong (p = 1/32) fail the accuracy gate even though
+    agreement stays above 99.5%; a balanced set of disagreements passes it."""
+    n = 1000
+    ref = [request(choice([0.6, 0.4])) for _ in range(n)]  # decides k0
+    cand = copy.deepcopy(ref)
+    gold = [{} for _ in range(n)]
+    for i in range(5):  # candidate flips to k1 on five gold-k0 questions (probabilities move too)
+        cand[i]["answers"]["q0"] = choice([0.4, 0.6])
+        gold[i]["q0"] = "k0"
+    stats = gates.agreement(cand, ref, gold)
+    assert stats["accuracy_test"] == {"wins": 0, "losses": 5, "p_value": 1 / 32, "accuracy": 0.0,
+                                      "reference_accuracy": 1.0}
+    assert stats["agreement"] == 0.995
+    failed = gates.failures(stats, {**gates.GATES, "probability_max": 1.0, "probability_mae": 1.0})
+    assert failed == ["accuracy sign test p 0.03125 < 0.05 (0 wins, 5 losses)"]
+    for i in range(5, 8):  # three flips where the candidate is right: 3 wins, 5 losses
+        cand[i]["answers"]["q0"] = choice([0.4, 0.6])
+        gold[i]["q0"] = "k1"
+    test = gates.agreement(cand, ref, gold)["accuracy_test"]
+    assert (test["wins"], test["losses"]) == (3, 5) and math.isclose(test["p_value"], 93 / 256)
+    # Without gold labels the accuracy gate does not apply.
+    assert "accuracy_test" not in gates.agreement(cand, ref)
+    with pytest.raises(ValueError):
+        gates.accuracy_test(cand, ref, gold[:-1])
