@@ -301,40 +301,33 @@ def run_engine_predict(path, args):
             "gpu_p50_ms": round(pct(gpu, 50), 4), "prepare_p50_ms": round(pct(prep, 50), 4)}
 
 
-def run_modernbert_predict(args):
+def run_modernbert_predict(path, args):
     """Engine.predict on a ModernBERT-base-shaped checkpoint at 83, 512 and 1,024 tokens: 22 layers,
     d=768, 12 heads, GeGLU 1152, RoPE, global attention every third layer and +-64 windows on the
     others, one head layer, random weights, the offline BPE tokenizer; every call tokenises, packs,
     runs and decodes.  Real Laya checkpoints are ModernBERT/mmBERT encoders whose dimensions the
     reference does not record, and its published predict latencies (README.md:13-16) are for those:
     context for them, not a like-for-like comparison."""
-    from laya_cuda import Engine, synthetic
-    root = tempfile.mkdtemp(prefix="laya_bench_mb_")
+    from laya_cuda import Engine
     out = {"model": "ModernBERT-base-shaped: 22L/768, 12 heads, GeGLU 1152, global every 3rd layer, +-64 windows, "
                     "RoPE 160000/10000, one head layer, fp16 operands; random weights, BPE tokenizer trained "
                     "offline; one 4-option choice question", "steps": args.steps}
-    try:
-        config = synthetic.modernbert_config(22, 768, 12, 1152, 50368, 8192)
-        task = dict(synthetic.task_config(1024), head_layers=1, head_max_len=64)
-        path = synthetic.checkpoint(root, config, task, seed=0, random_norms=False)[0]
-        with Engine(str(path), max_cached_shapes=4) as engine:
-            overhead = len(engine.adapter.prepare("", QUESTION)[0][0])
-            for target in (83, 512, 1024):
-                state = " refund" * max(1, target - overhead)
-                tokens = len(engine.adapter.prepare(state, QUESTION)[0][0])
-                for _ in range(args.warmup + 1):
-                    engine.predict(state, QUESTION)
-                api, gpu = [], []
-                for _ in range(args.steps):
-                    s = time.perf_counter()
-                    engine.predict(state, QUESTION)
-                    api.append((time.perf_counter() - s) * 1e3)
-                    gpu.append(engine.last_metrics["gpu_ms"])
-                out[f"tokens_{target}"] = {"tokens": tokens, "p50_ms": round(pct(api, 50), 4),
-                                           "p95_ms": round(pct(api, 95), 4), "gpu_p50_ms": round(pct(gpu, 50), 4)}
-                progress(f"modernbert-base {tokens} tokens: predict p50 {out[f'tokens_{target}']['p50_ms']} ms")
-    finally:
-        shutil.rmtree(root, ignore_errors=True)
+    with Engine(str(path), max_cached_shapes=4) as engine:
+        overhead = len(engine.adapter.prepare("", QUESTION)[0][0])
+        for target in (83, 512, 1024):
+            state = " refund" * max(1, target - overhead)
+            tokens = len(engine.adapter.prepare(state, QUESTION)[0][0])
+            for _ in range(args.warmup + 1):
+                engine.predict(state, QUESTION)
+            api, gpu = [], []
+            for _ in range(args.steps):
+                s = time.perf_counter()
+                engine.predict(state, QUESTION)
+                api.append((time.perf_counter() - s) * 1e3)
+                gpu.append(engine.last_metrics["gpu_ms"])
+            out[f"tokens_{target}"] = {"tokens": tokens, "p50_ms": round(pct(api, 50), 4),
+                                       "p95_ms": round(pct(api, 95), 4), "gpu_p50_ms": round(pct(gpu, 50), 4)}
+            progress(f"modernbert-base {tokens} tokens: predict p50 {out[f'tokens_{target}']['p50_ms']} ms")
     return out
 
 
@@ -418,6 +411,132 @@ def run_batching(path, args):
     return out
 
 
+# ---- the reference's latency suite (benchmarks/run.py:52-73, 127-151, 279-297) ----
+SUITE_QUESTION = {"type": "choice", "instructions": "Pick a topic.", "criteria": ["finance", "software"]}
+FILLER = " refund"
+
+
+def latency_cases(adapter):
+    """(name, state, questions) of the reference's latency cases: every length of 32-1,024 tokens that
+    fits max_len x 1, 5 and 10 questions, built from a repeated one-token word (the reference repeats
+    " investigation", one token for its checkpoints' tokenizers; " refund" is one for the offline
+    tokenizer) and checked to give exactly that many tokens; one question at 127, 129 and max_len - 1 tokens (the span boundaries); five
+    questions of different instruction lengths over a short state."""
+    def tokens(state, questions):
+        return len(adapter.prepare(state, questions)[0][0])
+
+    out = []
+    for length in (32, 64, 128, 256, 512, 768, 1024):
+        if length > adapter.max_len:
+            continue
+        for count in (1, 5, 10):
+            questions = {str(i): SUITE_QUESTION for i in range(count)}
+            state = FILLER * max(0, length - tokens("", questions))
+            if tokens(state, questions) != length:
+                raise RuntimeError(f"latency case l{length}-q{count} has {tokens(state, questions)} tokens")
+            out.append((f"l{length}-q{count}", state, questions))
+    single = {"0": SUITE_QUESTION}
+    for length in (127, 129, adapter.max_len - 1):
+        out.append((f"boundary-l{length}", FILLER * (length - tokens("", single)), single))
+    mixed = {str(i): {"type": "choice", "instructions": "Choose. " + "Different detail. " * i, "criteria": ["yes", "no"]}
+             for i in range(5)}
+    out.append(("mixed-lengths", "A support case about a payment.", mixed))
+    return out
+
+
+def suite_worker(args):
+    """One round of the suite in this fresh process: every latency case (first request, warm-up,
+    timed samples: p50/p95/p99 of Engine.predict and of the device time), in forward order on even
+    rounds and reversed on odd ones, then the 400 typed-decision requests of the fixed quality
+    fixture once each in fixture order (p50/p95/p99, and how many needed a new shape slot under
+    the default 16-slot cache)."""
+    import gzip
+    from laya_cuda import Engine
+    result = {"round": args.suite_round, "cases": {}}
+    start = time.perf_counter()
+    with Engine(args.suite_checkpoint) as engine:
+        result["load_ms"] = round((time.perf_counter() - start) * 1e3, 1)
+        cases = latency_cases(engine.adapter)
+        for name, state, questions in (cases if args.suite_round % 2 == 0 else cases[::-1]):
+            cold = time.perf_counter()
+            engine.predict(state, questions)
+            first_ms = (time.perf_counter() - cold) * 1e3
+            first = engine.last_metrics
+            for _ in range(args.warmup):
+                engine.predict(state, questions)
+            api, gpu = [], []
+            for _ in range(args.steps):
+                s = time.perf_counter()
+                engine.predict(state, questions)
+                api.append((time.perf_counter() - s) * 1e3)
+                gpu.append(engine.last_metrics["gpu_ms"])
+            result["cases"][name] = {
+                "tokens": engine.last_metrics["tokens_per_question"][0], "questions": len(questions),
+                "first_ms": round(first_ms, 3), "first_cache_miss": bool(first["cache_miss"]),
+                "p50_ms": round(pct(api, 50), 4), "p95_ms": round(pct(api, 95), 4), "p99_ms": round(pct(api, 99), 4),
+                "gpu_p50_ms": round(pct(gpu, 50), 4), "questions_per_s": round(len(questions) * 1e3 / np.mean(api), 1)}
+        fixture = json.loads(gzip.decompress((ROOT / "tests" / "golden" / "typed_decisions.json.gz").read_bytes()))
+        api, gpu, cold = [], [], 0
+        for row in fixture["records"]:
+            state, questions = json.loads(row["state"]), json.loads(row["questions"])
+            s = time.perf_counter()
+            engine.predict(state, questions)
+            api.append((time.perf_counter() - s) * 1e3)
+            gpu.append(engine.last_metrics["gpu_ms"])
+            cold += bool(engine.last_metrics["cache_miss"])
+        result["fixture"] = {"requests": len(api), "p50_ms": round(pct(api, 50), 4), "p95_ms": round(pct(api, 95), 4),
+                             "p99_ms": round(pct(api, 99), 4), "gpu_p50_ms": round(pct(gpu, 50), 4),
+                             "cold_shape_requests": cold}
+    Path(args.suite_out).write_text(json.dumps(result))
+
+
+def modernbert_base_checkpoint(root):
+    """ModernBERT-base-shaped checkpoint (22L/768, 12 heads, GeGLU 1152, max_len 1,024, one head layer)."""
+    from laya_cuda import synthetic
+    config = synthetic.modernbert_config(22, 768, 12, 1152, 50368, 8192)
+    task = dict(synthetic.task_config(1024), head_layers=1, head_max_len=64)
+    return synthetic.checkpoint(root, config, task, seed=0, random_norms=False)[0]
+
+
+def run_latency_suite(path, args):
+    """Three rounds of the suite, each in a fresh child process started one after another before
+    this process touches the GPU, on a ModernBERT-base-shaped checkpoint with max_len 1,024 (the
+    architecture family of the real Laya checkpoints; random weights, offline BPE tokenizer).  Per
+    case the rounds' p50/p95/p99 and first-request times are listed, with the median over rounds;
+    the fixture's 400 requests give the mixed-request p50/p95/p99 and cold-shape counts."""
+    import subprocess
+    root = tempfile.mkdtemp(prefix="laya_suite_")
+    rounds = []
+    try:
+        for r in range(3):
+            out = Path(root) / f"round{r}.json"
+            cmd = [sys.executable, str(ROOT / "bench.py"), "--suite-worker", "--suite-round", str(r),
+                   "--suite-checkpoint", str(path), "--suite-out", str(out), "--steps", str(args.steps),
+                   "--warmup", str(args.warmup)]
+            subprocess.run(cmd, check=True, timeout=600)
+            rounds.append(json.loads(out.read_text()))
+            progress(f"latency suite round {r}: fixture p50/p95/p99 {rounds[-1]['fixture']['p50_ms']}/"
+                     f"{rounds[-1]['fixture']['p95_ms']}/{rounds[-1]['fixture']['p99_ms']} ms, "
+                     f"{rounds[-1]['fixture']['cold_shape_requests']} cold")
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+    cases = {}
+    for name in rounds[0]["cases"]:
+        per = [rd["cases"][name] for rd in rounds]
+        cases[name] = {"tokens": per[0]["tokens"], "questions": per[0]["questions"],
+                       **{k: [p[k] for p in per] for k in ("p50_ms", "p95_ms", "p99_ms", "first_ms", "gpu_p50_ms")},
+                       "median_p50_ms": round(float(np.median([p["p50_ms"] for p in per])), 4),
+                       "median_p99_ms": round(float(np.median([p["p99_ms"] for p in per])), 4)}
+    fixture = [rd["fixture"] for rd in rounds]
+    return {"model": "ModernBERT-base-shaped: 22L/768, 12 heads, GeGLU 1152, global every 3rd layer, +-64 windows, "
+                     "max_len 1,024, one head layer, fp16 operands; random weights, offline BPE tokenizer",
+            "protocol": f"3 rounds in fresh processes (case order reversed on odd rounds), {args.warmup} warm-ups "
+                        f"and {args.steps} samples per case (the reference: 20 and 200)",
+            "load_ms": [rd["load_ms"] for rd in rounds], "cases": cases,
+            "cases_first_request_cold": sum(c["first_cache_miss"] for rd in rounds for c in rd["cases"].values()),
+            "fixture_requests": {k: [f[k] for f in fixture] for k in fixture[0]}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -426,17 +545,27 @@ def main():
     ap.add_argument("--stage-reps", type=int, default=10, help="eager forwards per stage for the stage timings")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="oracle time budget of the headline (0: none)")
     ap.add_argument("--only", default="", help="comma-separated subset of " + ",".join(
-        list(WORKLOADS) + ["engine", "batching", "modernbert"]) + " (default all; l512 is always the headline)")
+        list(WORKLOADS) + ["engine", "batching", "modernbert", "suite"]) + " (default all; l512 is always the headline)")
     ap.add_argument("--batching-requests", type=int, default=24, help="requests per closed-loop client")
     ap.add_argument("--eager", action="store_true", help="launch kernel by kernel instead of replaying hipGraphs")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a 64 MiB device copy (the reference size for HBM byte counters)")
+    ap.add_argument("--suite-worker", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--suite-round", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--suite-checkpoint", help=argparse.SUPPRESS)
+    ap.add_argument("--suite-out", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.suite_worker:
+        return suite_worker(args)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the encoder path shards by request with no collective, and "
               "multi-GPU runs are not implemented (use --gpus 1)", file=sys.stderr)
         sys.exit(2)
-    chosen = set(args.only.split(",")) if args.only else set(WORKLOADS) | {"engine", "batching", "modernbert"}
+    chosen = set(args.only.split(",")) if args.only else set(WORKLOADS) | {"engine", "batching", "modernbert", "suite"}
+    mb_root = tempfile.mkdtemp(prefix="laya_bench_mb_")
+    mb_path = modernbert_base_checkpoint(mb_root) if chosen & {"suite", "modernbert"} else None
+    # The latency suite's rounds run in fresh child processes, before this process touches the GPU.
+    suite = run_latency_suite(mb_path, args) if "suite" in chosen else None
     if args.calibrate_copy:
         import torch
         src = torch.ones(16 << 20, dtype=torch.float32, device="cuda:0")
@@ -473,7 +602,10 @@ def main():
         finally:
             shutil.rmtree(root, ignore_errors=True)
     if "modernbert" in chosen:
-        line["modernbert_base_predict"] = run_modernbert_predict(args)
+        line["modernbert_base_predict"] = run_modernbert_predict(mb_path, args)
+    shutil.rmtree(mb_root, ignore_errors=True)
+    if suite is not None:
+        line["latency_suite"] = suite
     print(json.dumps(line), flush=True)
 
 
