@@ -77,6 +77,23 @@ __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
 __device__ __forceinline__ void lds_load16(const void* g, unsigned lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds));
 }
+// The same direct load through a buffer resource (buffer_load_dwordx4 ... offen lds): lane l fetches
+// 16 bytes at resource base + voffset(l) + soffset and the hardware writes them to LDS byte address
+// lds + 16 l (lds wave-uniform, in M0).  Loads past the resource's byte range return zeros.
+__device__ __forceinline__ void lds_load16_buffer(i32x4 rsrc, unsigned voffset, unsigned soffset, unsigned lds) {
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voffset), "s"(rsrc), "s"(soffset),
+               "{m0}"(lds));
+}
+// 128-bit buffer resource of `bytes` bytes at `base` (raw buffer: stride 0, byte offsets), wave-uniform.
+__device__ __forceinline__ i32x4 buffer_resource(const void* base, unsigned bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(p & 0xffffffffu));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>((p >> 32) & 0xffffu));
+  r[2] = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+  r[3] = 0x00020000;  // dword 3 of a raw gfx9 buffer resource: 32-bit data format
+  return r;
+}
 // Byte address of an LDS object, as M0 wants it.
 __device__ __forceinline__ unsigned lds_address(const void* p) {
   typedef __attribute__((address_space(3))) const void* LdsPtr;
@@ -95,6 +112,11 @@ __device__ __forceinline__ void publish_stage() {
 // s_waitcnt immediate (gfx9 layout: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8) that waits
 // until at most `vm` vector memory operations are outstanding and every LDS access has completed.
 constexpr int waitcnt_vm(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
+// s_waitcnt immediate that waits until at most `vm` vector memory operations are outstanding and
+// leaves LDS accesses in flight.
+constexpr int waitcnt_vm_only(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (15 << 8); }
+// s_waitcnt immediate that waits for every LDS access (lgkmcnt 0) and no vector memory operation.
+constexpr int waitcnt_lgkm0_keep_vm() { return 15 | (3 << 14) | (7 << 4); }
 
 template <typename T> __device__ __forceinline__ T to_half(float v) { return static_cast<T>(v); }
 template <typename T> __device__ __forceinline__ float to_float(T v) { return static_cast<float>(v); }

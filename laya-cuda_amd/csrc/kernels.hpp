@@ -86,6 +86,9 @@ constexpr int kBatchedRows = 4096;
 void gemm_plan(int M, int N, int K, Epi epi, DType t, int cus, int* tile, int* splits, bool rope = false,
                bool measured = true);
 hipError_t gemm_prepare();  // sets LDS attributes of the large-tile kernels (call once per device)
+// Pipelined tiles read their operands through buffer resources with 32-bit byte offsets: true when
+// both operands ([M][lda] and [N][ldb] 16-bit) span fewer than 2^32 bytes.
+bool gemm_operands_addressable(long long M, long long lda, long long N, long long ldb);
 hipError_t launch_gemm(const GemmArgs& a, Epi epi, DType t, int tile, hipStream_t stream);
 
 // ---- fused bidirectional attention over packed rows ----

@@ -22,6 +22,7 @@
 #include "kernels.hpp"
 #include "laya_hip.h"
 #include "packing.hpp"
+#include "scope.hpp"
 
 // Device scratch of laya_predict_static: the whole shape-slot arena of one forward (packed block,
 // activations, split-K partials, head buffers) for callers that cannot allocate.  The loader gives
@@ -319,6 +320,8 @@ void plan_slot(const Engine& E, Slot* s, int m, int b, int k) {
   s->k = k;
   s->L = make_layout(m, b, k);
   const int d = c.width, f = c.intermediate;
+  LAYA_REQUIRE(gemm_operands_addressable(m, std::max(f, 4 * d), std::max(3 * d, 4 * d), std::max(f, 4 * d)),
+               "a shape class of " + std::to_string(m) + " packed rows exceeds the 4 GiB GEMM operand limit");
   gemm_plan(m, 3 * d, d, Epi::QKV, E.mfma(), E.cus, &s->tile[0], &s->splits[0], E.modern);
   gemm_plan(m, d, d, Epi::F32, E.mfma(), E.cus, &s->tile[1], &s->splits[1]);
   if (E.modern) {
@@ -688,11 +691,12 @@ void forward(Engine& E, Slot& s, int marked = -1, hipEvent_t* marks = nullptr) {
       launch_timing = LaunchTiming{marks[2 * mark], marks[2 * mark + 1]};
       ++mark;
     }
+    // However the stage ends (a launch that fails before its kernel takes the events throws), no
+    // event pair stays armed for a later launch on this thread: the caller destroys the events.
+    const ScopeExit disarm([&] { if (timed) launch_timing = LaunchTiming{}; });
     launch_stage(E, s, stage, layer);
-    if (timed && launch_timing.start) {  // the stage launched nothing (no rows): nothing to time
-      launch_timing = LaunchTiming{};
+    if (timed && launch_timing.start)  // the stage launched nothing (no rows): nothing to time
       throw Failure{LAYA_EINVAL, "timed stage launched no kernel"};
-    }
   };
   run(kEmbed, 0);
   for (int i = 0; i < E.cfg.layers; ++i)
@@ -1163,6 +1167,9 @@ int laya_predict_static(void* handle, const int32_t* host_packed, const LayaShap
     char* base = static_cast<char*>(g_scratch[E->device]);
     LAYA_REQUIRE(base != nullptr, "device scratch not set up");
     std::lock_guard<std::mutex> lock(g_static_mutex);
+    // On any error below, the copies and kernels already queued may still write the shared scratch:
+    // drain the stream before the lock is released, so the next caller's work cannot overlap them.
+    ScopeExit drain([&] { (void)hipStreamSynchronize(E->stream); });
     carve_slot(*E, &s, base);
     s.h_packed = g_static_stage;
     std::memcpy(s.h_packed, host_packed, s.L.user_end * 4);
@@ -1176,6 +1183,7 @@ int laya_predict_static(void* handle, const int32_t* host_packed, const LayaShap
                               static_cast<size_t>(k) * 4, b, hipMemcpyDeviceToHost, E->stream));
     LAYA_HIP(hipMemcpyAsync(host_acts, s.acts, static_cast<size_t>(b) * E->cfg.n_act * 4, hipMemcpyDeviceToHost,
                             E->stream));
+    drain.release();
     LAYA_HIP(hipStreamSynchronize(E->stream));
     float ms = 0.f;
     LAYA_HIP(hipEventElapsedTime(&ms, E->static_start, E->static_end));
