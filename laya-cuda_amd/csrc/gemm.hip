@@ -93,12 +93,25 @@ __device__ __forceinline__ void load_early_pos(const GemmArgs& a, int row, int (
 // Epilogue shared by both GEMM kernels: acc holds this wave's (BM/WM) x (BN/WN) block of C^T as
 // 32x32 MFMA tiles; smem_raw must have kEpilogueStageBytes per wave free (the caller's main loop is
 // done with LDS: its last barrier has passed).
-template <typename T, int BM, int BN, int WM, int WN, Epi E, bool kEarlyBias>
+// acc[i][j][4 r4 + e] holds element e of the lane's column quad r4 of 32x32 output region (i, j):
+// with 32x32x16 MFMAs (L16 false) row lane % 32, columns 8 r4 + 4 (lane / 32) .. +3; with 16x16x32
+// MFMAs (L16 true; quad r4 is the 16x16 block (r4 / 2, r4 % 2) of the region) row 16 (r4 / 2) +
+// lane % 16, columns 16 (r4 % 2) + 4 (lane % 64 / 16) .. +3.
+template <bool L16>
+__device__ __forceinline__ int quad_row(int lane, int r4) { return L16 ? ((r4 >> 1) << 4) + (lane & 15) : lane & 31; }
+template <bool L16>
+__device__ __forceinline__ int quad_col(int lane, int r4) {
+  return L16 ? ((r4 & 1) << 4) + ((lane >> 4) << 2) : 8 * r4 + 4 * (lane >> 5);
+}
+
+template <typename T, int BM, int BN, int WM, int WN, Epi E, bool kEarlyBias, bool L16 = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
                                               const float4 (&early_bias)[kEarlyBias ? BN / WN / 32 : 1][4],
                                               const int (&early_pos)[BM / WM / 32], int m0, int n0, int z,
                                               unsigned char* smem_raw, int lane, int wave) {
   constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+  static_assert(!L16 || (E != Epi::GEGLU && E != Epi::QKV_ROPE && !kEarlyBias),
+                "the 16x16 accumulator order serves the row-major and head-major epilogues without RoPE");
   const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
   const int lrow = lane & 31, kg = lane >> 5;
   const bool with_bias = (E != Epi::F32 || a.splits == 1) && a.bias;
@@ -112,7 +125,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[B
     v[3] = acc[i][j][4 * r4 + 3];
     if (with_bias) {
       const float4 b = kEarlyBias ? early_bias[kEarlyBias ? j : 0][r4]
-                                  : *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + j * 32 + 8 * r4 + 4 * kg);
+                                  : *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + j * 32 + quad_col<L16>(lane, r4));
       v[0] = v[0] + b.x; v[1] = v[1] + b.y; v[2] = v[2] + b.z; v[3] = v[3] + b.w;
     }
   };
@@ -153,12 +166,13 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[B
   typedef typename std::conditional<E == Epi::F32, float, T>::type S;
   S* stg = reinterpret_cast<S*>(smem_raw) + wave * 32 * SP;
   const int rbase = m0 + wm0;  // first output row of this wave
-  // Row-major 32x32 tile: lane values h[r4] = columns 8 r4 + 4 kg .. +3 of tile row lrow; chunk
+  // Row-major 32x32 tile: lane values h[r4] = the column quad r4 (quad_row, quad_col); chunk
   // (r, c) (tile row r, first column c) is stored at dst(row, c) when row = rbase + 32 i + r < M.
   auto emit_rows = [&](int i, const auto (&h)[4], auto dst) {
     typedef typename std::remove_cv<typename std::remove_reference<decltype(h[0])>::type>::type Q;
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) *reinterpret_cast<Q*>(stg + lrow * SP + 8 * r4 + 4 * kg) = h[r4];
+    for (int r4 = 0; r4 < 4; ++r4)
+      *reinterpret_cast<Q*>(stg + quad_row<L16>(lane, r4) * SP + quad_col<L16>(lane, r4)) = h[r4];
     constexpr int EPC = 16 / sizeof(S), CPR = 32 / EPC;  // elements per chunk, chunks per row
 #pragma unroll
     for (int t = 0; t < 32 * CPR / 64; ++t) {
@@ -253,7 +267,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[B
             float v[4];
             take(i, j, r4, v);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) stg[(8 * r4 + 4 * kg + e) * SP + lrow] = to_half<T>(v[e]);
+            for (int e = 0; e < 4; ++e)
+              stg[(quad_col<L16>(lane, r4) + e) * SP + quad_row<L16>(lane, r4)] = to_half<T>(v[e]);
           }
 #pragma unroll
           for (int t = 0; t < 2; ++t) {
@@ -476,7 +491,7 @@ __device__ __forceinline__ int swz_k(int row) {
 // wave tiles whose accumulators alone take 256 registers: 8-wave workgroups own a CU, 4-wave ones
 // with smaller wave tiles share it with a second workgroup (whose main loop then covers this one's
 // epilogue).
-template <typename T, int BM, int BN, int WM, int WN, int BKS, int S, Epi E, bool RING>
+template <typename T, int BM, int BN, int WM, int WN, int BKS, int S, Epi E, bool RING, bool M16 = false>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(BM * BN / (WM * WN) >= 128 * 128 ? 1 : 2)))
 void gemm_pipe_kernel(GemmArgs a) {
   constexpr int NW = WM * WN;
@@ -632,7 +647,93 @@ void gemm_pipe_kernel(GemmArgs a) {
   constexpr int KPRE = KS - 1;
   constexpr int LPS = (NLD + KPRE - 1) / KPRE;  // loads per pre-barrier k-step
 
-  if (RING && n > 0) {
+  if constexpr (M16) {
+    // The ring below with 16x16x32 MFMAs: each wave's (BM/WM) x (BN/WN) block is (2 TM) x (2 TN)
+    // blocks of 16x16, a k-step is 32 deep (lane l feeds k 8 (l / 16) .. +7 of row l % 16), so a
+    // 64-deep slab is two k-steps of 4 TN TM MFMAs and 2 (TM + TN) LDS reads: the same LDS bytes
+    // as the 32x32x16 form, but the MFMA stream measured 5-7% faster on the 64K-row projections
+    // (register-only streams: 2.06 against 1.80 PFLOP/s on random operands, two waves per SIMD).
+    static_assert(RING && BKS == 64, "16x16x32 MFMAs: the ring with 64-deep slabs");
+    constexpr int KS16 = BKS / 32, MB = TM * 2, NB = TN * 2;
+    T8 a16[2][MB], b16[2][NB];
+    f32x4 acc16[MB][NB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) acc16[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int l16 = lane & 15, kq = lane >> 4;
+    auto fetch16 = [&](const T* cA, const T* cB, int kk, int s) {
+      const int ch = kk * 4 + kq;
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        const int r = wm0 + i * 16 + l16;
+        a16[s][i] = *reinterpret_cast<const T8*>(cA + r * BKS + ((ch ^ swz_k<BKS>(r)) << 3));
+      }
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int r = wn0 + j * 16 + l16;
+        b16[s][j] = *reinterpret_cast<const T8*>(cB + r * BKS + ((ch ^ swz_k<BKS>(r)) << 3));
+      }
+    };
+    auto mma16 = [&](int s) {  // weights as the A operand: the accumulator holds C^T
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc16[i][j] = ::laya::mfma16(b16[s][j], a16[s][i], acc16[i][j]);
+    };
+    auto interleave16 = [&]() {  // two LDS reads per MFMA slot, first
+#pragma unroll
+      for (int t = 0; t < MB * NB; ++t) {
+        if (2 * t < MB + NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (2 * t + 1 < MB + NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+    };
+    if (n > 0) {
+#pragma unroll
+      for (int h = 0; h < 5; ++h) {
+        const int kt = kb + min(h / 2, n - 1);
+#pragma unroll
+        for (int q = (h & 1) ? AG : 0; q < ((h & 1) ? NLD : AG); ++q) issue_ring(q, kt, h);
+      }
+      publish_stage<kWaitFirst>();
+      fetch16(lds, lds + HALFE, 0, 0);
+      int abuf = 0;
+      for (int it = 0; it < n; ++it) {
+        const int bbuf = abuf == 4 ? 0 : abuf + 1;
+        const int nabuf = abuf >= 3 ? abuf - 3 : abuf + 2, nbbuf = nabuf == 4 ? 0 : nabuf + 1;
+#pragma unroll
+        for (int kk = 0; kk < KS16 - 1; ++kk) {
+          fetch16(lds + abuf * HALFE, lds + bbuf * HALFE, kk + 1, (kk + 1) & 1);
+          mma16(kk & 1);
+          interleave16();
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        publish_stage<kWaitSlab>();
+        __builtin_amdgcn_sched_barrier(0);
+        fetch16(lds + nabuf * HALFE, lds + nbbuf * HALFE, 0, 0);
+        const int kt2 = kb + min(it + 2, n - 1), kt3 = kb + min(it + 3, n - 1);
+#pragma unroll
+        for (int q = AG; q < NLD; ++q) issue_ring(q, kt2, abuf);
+#pragma unroll
+        for (int q = 0; q < AG; ++q) issue_ring(q, kt3, bbuf);
+        mma16((KS16 - 1) & 1);
+        interleave16();
+        __builtin_amdgcn_sched_barrier(0);
+        abuf = nabuf;
+      }
+    }
+    // Quad r4 of 32x32 region (i, j) is 16x16 block (2 i + r4 / 2, 2 j + r4 % 2) (quad_row/quad_col).
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] = acc16[2 * i + (q >> 1)][2 * j + (q & 1)][e];
+  }
+  if (RING && !M16 && n > 0) {
     // Ring of five half-slab buffers (160 KB for 256x256 tiles): half h (slab h / 2, A rows for
     // even h, B rows for odd) lives in buffer h % 5.  While slab it is consumed from halves 2it and
     // 2it+1, halves 2it+2 .. 2it+4 are landed or in flight; the barrier after its last LDS reads
@@ -714,7 +815,8 @@ void gemm_pipe_kernel(GemmArgs a) {
   // reuses LDS.
   __builtin_amdgcn_s_waitcnt(kWaitAll);
   __syncthreads();
-  gemm_epilogue<T, BM, BN, WM, WN, E, kEarlyBias>(a, acc, early_bias, early_pos, m0, n0, z, smem_raw, lane, wave);
+  gemm_epilogue<T, BM, BN, WM, WN, E, kEarlyBias, M16>(a, acc, early_bias, early_pos, m0, n0, z, smem_raw, lane,
+                                                       wave);
 }
 
 struct TileDef {
@@ -722,6 +824,7 @@ struct TileDef {
   int pf;      // >= 2: register-staged kernel with pf slabs in flight; 0: pipelined direct-to-LDS kernel
   int bk, st;  // pipelined kernel: slab depth and LDS stages (ring: five half-slab buffers)
   bool ring;
+  bool m16 = false;  // ring with 16x16x32 MFMAs (row-major and head-major epilogues without RoPE)
   int threads() const { return 64 * wm * wn; }
 };
 // Tile menu; the planner picks per problem.  Ids are part of the op-level ABI (tests sweep them).
@@ -757,6 +860,8 @@ constexpr TileDef kTiles[] = {
     // batch: 240 tiles of 256x192 for N = 768 instead of 180 of 256x256): 12.5% fewer operand bytes
     // per tile, in a two-stage pipeline (the ring needs square tiles).
     {256, 192, 4, 2, 0, 64, 2},  // 21: 8 waves of 64x96
+    // Tile 19 with 16x16x32 MFMAs (faster MFMA stream, same LDS traffic); not for RoPE or GeGLU.
+    {256, 256, 2, 4, 0, 64, 5, true, true},  // 22
 };
 constexpr int kTileCount = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -800,6 +905,10 @@ hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
     LAYA_RING(19, 256, 256, 2, 4)
     LAYA_RING(20, 256, 256, 2, 2)
     LAYA_PIPE(21, 256, 192, 4, 2, 64, 2)
+    case 22:
+      if constexpr (E == Epi::GEGLU || E == Epi::QKV_ROPE) return hipErrorInvalidValue;
+      else LAYA_LAUNCH((gemm_pipe_kernel<T, 256, 256, 2, 4, 64, 5, E, true, true>), grid, block, lds, stream, a);
+      break;
 #undef LAYA_RING
 #undef LAYA_TILE
 #undef LAYA_PIPE
@@ -832,6 +941,9 @@ hipError_t set_lds_attr() {
   LAYA_ATTR(19, gemm_pipe_kernel<T, 256, 256, 2, 4, 64, 5, E, true>)
   LAYA_ATTR(20, gemm_pipe_kernel<T, 256, 256, 2, 2, 64, 5, E, true>)
   LAYA_ATTR(21, gemm_pipe_kernel<T, 256, 192, 4, 2, 64, 2, E, false>)
+  if constexpr (E != Epi::GEGLU && E != Epi::QKV_ROPE) {
+    LAYA_ATTR(22, gemm_pipe_kernel<T, 256, 256, 2, 4, 64, 5, E, true, true>)
+  }
 #undef LAYA_ATTR
   return e;
 }
@@ -915,6 +1027,9 @@ void gemm_plan(int M, int N, int K, Epi epi, DType t, int cus, int* tile, int* s
       }
     }
     if (best_cost >= 0) {
+      // The ring with 16x16x32 MFMAs for the row-major epilogues: out/down 2-6%, up 5% faster on
+      // 64K rows; the head-major QKV epilogue measured 4% slower with it, so QKV keeps tile 19.
+      if (best == 19 && (epi == Epi::F32 || epi == Epi::HALF || epi == Epi::GELU || epi == Epi::RELU)) best = 22;
       *tile = best;
       *splits = 1;
       return;
@@ -957,6 +1072,7 @@ hipError_t launch_gemm(const GemmArgs& args, Epi epi, DType t, int tile, hipStre
   if (epi == Epi::QKV && a.rope_cos) epi = Epi::QKV_ROPE;
   // RoPE needs both halves of a head in one lane: wave tiles of 64-column multiples.
   const TileDef& td = kTiles[tile];
+  if (td.m16 && (epi == Epi::QKV_ROPE || epi == Epi::GEGLU)) return hipErrorInvalidValue;
   if (epi == Epi::QKV_ROPE && (td.bn / td.wn) % 64) return hipErrorInvalidValue;
   if ((epi == Epi::QKV || epi == Epi::QKV_ROPE) && a.M % 8) return hipErrorInvalidValue;  // V^T: runs of 8 tokens
   if (epi == Epi::GEGLU && (a.N % 32 || a.ldo * 2 < a.N)) return hipErrorInvalidValue;

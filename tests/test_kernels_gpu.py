@@ -240,7 +240,7 @@ def linear(x, w, bias, out, kind, dtype, M, N, K, splits, tile):
     sync()
 
 
-GEMM_TILES = 22  # tile ids of laya_op_linear (csrc/gemm.hip kTiles)
+GEMM_TILES = 23  # tile ids of laya_op_linear (csrc/gemm.hip kTiles)
 TILE_BN = {21: 192}  # tiles whose width is not a power of two
 
 
@@ -328,7 +328,29 @@ def test_linear_gelu_epilogue(gpu, dtype):
     np.testing.assert_allclose(from16(out), expected, atol=tol, rtol=tol)
 
 
-@pytest.mark.parametrize("tile", [0, 2, 5, 6, 7, 9, 11, 12, 13, 14, 16, 18, 19, 20, 21])
+def test_sixteen_wide_mfma_tile_refuses_rope_and_geglu(gpu):
+    """Tile 22 (the ring with 16x16x32 MFMAs) serves the row-major and head-major epilogues; the
+    GeGLU and RoPE epilogues, which assume the 32x32 accumulator order, are refused with an error
+    instead of running."""
+    t = torch()
+    M, width = 256, 256
+    x = t.zeros((M, width), dtype=t.float16, device=gpu)
+    w = t.zeros((2 * width, width), dtype=t.float16, device=gpu)
+    out = t.zeros((M, width), dtype=t.float16, device=gpu)
+    lib = _lib.load()
+    assert lib.laya_op_linear(p(x), p(w), None, p(out), 4, _lib.F16, M, 2 * width, width, 1, 22, stream()) != 0
+    wq = t.zeros((3 * width, width), dtype=t.float16, device=gpu)
+    q, k, vt = (t.zeros((M * width,), dtype=t.float16, device=gpu) for _ in range(3))
+    cos, sin = t.ones((M, 32), device=gpu), t.zeros((M, 32), device=gpu)
+    pos = t.zeros(M, dtype=t.int32, device=gpu)
+    assert lib.laya_op_qkv(p(x), p(wq), None, p(q), p(k), p(vt), p(cos), p(sin), p(pos), _lib.F16, M, width, 22,
+                           stream()) != 0
+    assert lib.laya_op_qkv(p(x), p(wq), None, p(q), p(k), p(vt), None, None, None, _lib.F16, M, width, 22,
+                           stream()) == 0
+    sync()
+
+
+@pytest.mark.parametrize("tile", [0, 2, 5, 6, 7, 9, 11, 12, 13, 14, 16, 18, 19, 20, 21, 22])
 def test_qkv_epilogue_writes_head_major_layout(gpu, tile):
     """Integer-valued operands make the product exact, so the layout check is bit-exact."""
     t = torch()
