@@ -157,9 +157,7 @@ int laya_predict_static(void* handle, const int32_t* host_packed, const LayaShap
  * (attn_norm, ffn_norm) change the residual on every repetition: time them, do not read results
  * afterwards.  layer = -1 times the stage where it runs: `reps` eager forwards in which every
  * kernel of the stage (all its layers) records the start and end of its own execution
- * (hipExtLaunchKernel events, the interval a kernel trace reports; the stream drains before each
- * such launch, so its start is not taken while the kernel before it still runs); *avg_ms is their
- * average. */
+ * (hipExtLaunchKernel events, the interval a kernel trace reports); *avg_ms is their average. */
 int laya_stage_count(void);
 const char* laya_stage_name(int stage);
 /* How many times this engine's forward launches `stage` (0: not part of this model) and the first

@@ -688,10 +688,6 @@ void forward(Engine& E, Slot& s, int marked = -1, hipEvent_t* marks = nullptr) {
   auto run = [&](int stage, int layer) {
     const bool timed = marks && stage == marked;
     if (timed) {
-      // The stream drains first: queued behind a running kernel, a dispatch's start timestamp would
-      // be taken while its predecessor still runs (about 1 us early at batch 1), and the interval
-      // would no longer be the kernel's own, the one a kernel trace reports.
-      LAYA_HIP(hipStreamSynchronize(E.stream));
       launch_timing = LaunchTiming{marks[2 * mark], marks[2 * mark + 1]};
       ++mark;
     }
