@@ -862,6 +862,12 @@ constexpr TileDef kTiles[] = {
     {256, 192, 4, 2, 0, 64, 2},  // 21: 8 waves of 64x96
     // Tile 19 with 16x16x32 MFMAs (faster MFMA stream, same LDS traffic); not for RoPE or GeGLU.
     {256, 256, 2, 4, 0, 64, 5, true, true},  // 22
+    // Eight-wave forms of the pipelined batch-1 tiles: a CU's direct loads from L2 run about twice
+    // as fast from eight waves as from four (45-49 against 22-25 bytes per clock in a streaming
+    // probe), and at batch 1 each CU's operand stream is what bounds a tile.
+    {128, 64, 4, 2, 0, 64, 6},   // 23: 8 waves of 32x32
+    {64, 128, 2, 4, 0, 64, 6},   // 24: 8 waves of 32x32
+    {128, 128, 4, 2, 0, 64, 4},  // 25: 8 waves of 32x64
 };
 constexpr int kTileCount = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -909,6 +915,9 @@ hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
       if constexpr (E == Epi::GEGLU || E == Epi::QKV_ROPE) return hipErrorInvalidValue;
       else LAYA_LAUNCH((gemm_pipe_kernel<T, 256, 256, 2, 4, 64, 5, E, true, true>), grid, block, lds, stream, a);
       break;
+    LAYA_PIPE(23, 128, 64, 4, 2, 64, 6)
+    LAYA_PIPE(24, 64, 128, 2, 4, 64, 6)
+    LAYA_PIPE(25, 128, 128, 4, 2, 64, 4)
 #undef LAYA_RING
 #undef LAYA_TILE
 #undef LAYA_PIPE
@@ -944,6 +953,9 @@ hipError_t set_lds_attr() {
   if constexpr (E != Epi::GEGLU && E != Epi::QKV_ROPE) {
     LAYA_ATTR(22, gemm_pipe_kernel<T, 256, 256, 2, 4, 64, 5, E, true, true>)
   }
+  LAYA_ATTR(23, gemm_pipe_kernel<T, 128, 64, 4, 2, 64, 6, E, false>)
+  LAYA_ATTR(24, gemm_pipe_kernel<T, 64, 128, 2, 4, 64, 6, E, false>)
+  LAYA_ATTR(25, gemm_pipe_kernel<T, 128, 128, 4, 2, 64, 4, E, false>)
 #undef LAYA_ATTR
   return e;
 }

@@ -3,7 +3,9 @@
 For every encoder shape family below, every packed-row class up to 2,048 rows (the classes
 laya_cuda.runtime rounds requests to) and both MFMA input types, each GEMM of the forward is timed
 through the op-level C ABI (laya_op_linear / laya_op_qkv) with every tile id and, for the fp32
-split-K epilogue, 1/2/4/8 splits, and also with the library's own heuristic plan (tile -2).  A
+split-K epilogue, 1/2/4/8 splits, and also with the library's own heuristic plan (tile -2); the
+launches take twelve input and weight matrices in turn, so each reads its operands from beyond L2
+as a forward does.  A
 problem gets a table row only when the best measured launch beats the heuristic by more than 3%;
 the library looks rows up at slot creation (exact match on CUs, M, N, K, epilogue, type, RoPE).
 
@@ -27,6 +29,8 @@ from laya_cuda import _lib  # noqa: E402
 F32, HALF, GELU, QKV, RELU, GEGLU = 0, 1, 2, 3, 4, 5
 KIND = {F32: 0, HALF: 1, GELU: 2, RELU: 3, GEGLU: 4}
 DTYPE_ID = {"f16": 1, "bf16": 2}  # kernels.hpp DType
+
+LAYERS = 12  # weight matrices timed in turn
 
 # (name, width d, FFN width f, ModernBERT variant)
 FAMILIES = [("bert-768", 768, 3072, False), ("bert-1024", 1024, 4096, False), ("modernbert-768", 768, 1152, True)]
@@ -83,8 +87,11 @@ def main():
             tdt = torch.float16 if dtype == "f16" else torch.bfloat16
             lib_dtype = _lib.F16 if dtype == "f16" else _lib.BF16
             for epi, N, K, rope in problems(d, f, modern):
-                x = torch.zeros(maxm, K, device=dev, dtype=tdt)
-                w = (torch.randn(N, K, device=dev) * 0.02).to(tdt)
+                # One input and one weight matrix per layer, used in turn: as in a forward, each launch
+                # reads operands that are not in its L2 (a loop over one pair would time L2-resident ones).
+                xs = [torch.zeros(maxm, K, device=dev, dtype=tdt) for _ in range(LAYERS)]
+                ws = [(torch.randn(N, K, device=dev) * 0.02).to(tdt) for _ in range(LAYERS)]
+                turn = [0]
                 out = torch.zeros(8 * maxm * N, device=dev)  # fp32 partials, or 16-bit outputs
                 cos = torch.ones(maxm, 32, device=dev) if rope else None
                 sin = torch.zeros(maxm, 32, device=dev) if rope else None
@@ -96,13 +103,17 @@ def main():
                     seen.add(key)
 
                     def launch(tile, splits):
-                        if epi == QKV:
-                            third = M * (N // 3) // 2  # fp32 slots holding M*(N/3) 16-bit values
-                            q, k, vt = out[:third], out[third:2 * third], out[2 * third:3 * third]
-                            return lambda: lib.laya_op_qkv(p(x), p(w), None, p(q), p(k), p(vt), p(cos), p(sin), p(pos),
-                                                           lib_dtype, M, N // 3, tile, stream)
-                        return lambda: lib.laya_op_linear(p(x), p(w), None, p(out), KIND[epi], lib_dtype, M, N, K,
-                                                          splits, tile, stream)
+                        def call():
+                            x, w = xs[turn[0] % LAYERS], ws[turn[0] % LAYERS]
+                            turn[0] += 1
+                            if epi == QKV:
+                                third = M * (N // 3) // 2  # fp32 slots holding M*(N/3) 16-bit values
+                                q, k, vt = out[:third], out[third:2 * third], out[2 * third:3 * third]
+                                return lib.laya_op_qkv(p(x), p(w), None, p(q), p(k), p(vt), p(cos), p(sin), p(pos),
+                                                       lib_dtype, M, N // 3, tile, stream)
+                            return lib.laya_op_linear(p(x), p(w), None, p(out), KIND[epi], lib_dtype, M, N, K, splits,
+                                                      tile, stream)
+                        return call
                     heuristic = timed(launch(-2, 1))
                     best = None
                     for tile in range(64):  # ids past the tile menu are refused (not timed)
@@ -119,12 +130,17 @@ def main():
                         rows.append((cus, M, N, K, epi, DTYPE_ID[dtype], int(rope), best[1], best[2], heuristic, best[0]))
                     print(f"{name} {dtype} epi {epi} M={M} N={N} K={K} rope={int(rope)}: heuristic {heuristic:.2f} us, "
                           f"best t{best[1]} s{best[2]} {best[0]:.2f} us ({gain * 100:+.1f}%)", flush=True)
-                del x, w, out
+                del xs, ws, out
                 torch.cuda.empty_cache()
     with open(args.out, "w") as fh:
-        fh.write("// Measured GEMM plans: {CUs, M, N, K, epilogue, MFMA type, RoPE, tile, splits}.  Written by\n"
-                 f"// tune_gemm_plans.py on {torch.cuda.get_device_name(0)} ({cus} CUs); rows only where the measured\n"
-                 "// launch beat the heuristic plan by more than 3% (heuristic -> measured us per launch).\n")
+        fh.write("// Measured GEMM plans: {CUs, M, N, K, epilogue, MFMA type, RoPE, tile, splits}.  Each GEMM of the\n"
+                 f"// forward at every packed-row class up to {maxm:,} rows was timed on {torch.cuda.get_device_name(0)} "
+                 f"({cus} CUs)\n"
+                 "// through laya_op_linear / laya_op_qkv with every tile id (and 1/2/4/8 splits for the fp32 split-K\n"
+                 "// epilogue) against the heuristic plan (tile -2); a row is kept only where the best measured\n"
+                 "// launch beat the heuristic by more than 3% (heuristic -> measured us per launch).  Regenerate on\n"
+                 "// the target GPU from the repository root with  python laya-cuda_amd/csrc/tune_gemm_plans.py\n"
+                 "// (it rewrites this file), then rebuild the library.\n")
         for cus_, M, N, K, epi, dt, rope, tile, splits, h, b in rows:
             fh.write(f"    {{{cus_}, {M}, {N}, {K}, {epi}, {dt}, {rope}, {tile}, {splits}}},  // {h:.2f} -> {b:.2f}\n")
     print(f"{len(rows)} plans written to {args.out} in {time.time() - began:.0f} s", flush=True)

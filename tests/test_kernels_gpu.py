@@ -240,7 +240,7 @@ def linear(x, w, bias, out, kind, dtype, M, N, K, splits, tile):
     sync()
 
 
-GEMM_TILES = 23  # tile ids of laya_op_linear (csrc/gemm.hip kTiles)
+GEMM_TILES = 26  # tile ids of laya_op_linear (csrc/gemm.hip kTiles)
 TILE_BN = {21: 192}  # tiles whose width is not a power of two
 
 
