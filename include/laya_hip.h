@@ -155,9 +155,10 @@ int laya_predict_static(void* handle, const int32_t* host_packed, const LayaShap
  * stage `stage` of layer `layer` `reps` times back to back between two events on the engine's
  * stream and stores the average per launch in *avg_ms.  Stages that normalise in place
  * (attn_norm, ffn_norm) change the residual on every repetition: time them, do not read results
- * afterwards.  layer = -1 times the stage where it runs: `reps` eager forwards in which every
- * kernel of the stage (all its layers) records the start and end of its own execution
- * (hipExtLaunchKernel events, the interval a kernel trace reports); *avg_ms is their average. */
+ * afterwards.  layer = -1 times the stage where it runs: `reps` (at most 1000) eager forwards,
+ * queued back to back, in which every kernel of the stage (all its layers) records the start and
+ * end of its own execution (hipExtLaunchKernel events, the interval a kernel trace reports);
+ * *avg_ms is their average. */
 int laya_stage_count(void);
 const char* laya_stage_name(int stage);
 /* How many times this engine's forward launches `stage` (0: not part of this model) and the first

@@ -1226,25 +1226,30 @@ int laya_time_stage(void* handle, const int32_t* host_packed, const LayaShape* s
     LAYA_REQUIRE(avg_ms && reps >= 1 && reps <= 100000, "reps must be in [1, 100000]");
     LAYA_REQUIRE(stage >= 0 && stage < kStageCount, "unknown stage");
     if (layer == -1) {  // in-forward timing: every kernel of the stage inside `reps` eager forwards
+      LAYA_REQUIRE(reps <= 1000, "in-forward timing takes at most 1000 forwards");
       int launches = 0;
       const int span = per_layer(stage) ? E->cfg.layers : per_head_layer(stage) ? E->cfg.head_layers : 1;
       for (int j = 0; j < span; ++j) launches += stage_used(*E, stage, j);
       LAYA_REQUIRE(launches > 0, "stage not in this model's forward");
       bool miss = false;
       Slot* s = stage_inputs(E, host_packed, shape, &miss);
-      std::vector<hipEvent_t> marks(2 * static_cast<size_t>(launches), nullptr);
+      // One event pair per timed launch of every repetition, the forwards queued back to back
+      // behind the warm one and read after a single synchronisation.  The events skip the
+      // system-scope fence (timing only): with it, each recording wrote back and invalidated the
+      // caches around the timed kernel, which in a kernel trace then started after a 12 us gap and
+      // ran 15.3 against 13.5 us (the 1,024-token attention) - no longer the forward's kernel.
+      const size_t pairs = static_cast<size_t>(launches) * reps;
+      std::vector<hipEvent_t> marks(2 * pairs, nullptr);
       double total = 0.0;
       try {
-        for (hipEvent_t& e : marks) LAYA_HIP(hipEventCreate(&e));
+        for (hipEvent_t& e : marks) LAYA_HIP(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
         forward(*E, *s);  // warm: the first forward of a fresh slot pays first-touch costs
-        for (int r = 0; r < reps; ++r) {
-          forward(*E, *s, stage, marks.data());
-          LAYA_HIP(hipStreamSynchronize(E->stream));
-          for (int i = 0; i < launches; ++i) {
-            float ms = 0.f;
-            LAYA_HIP(hipEventElapsedTime(&ms, marks[2 * i], marks[2 * i + 1]));
-            total += ms;
-          }
+        for (int r = 0; r < reps; ++r) forward(*E, *s, stage, marks.data() + 2 * static_cast<size_t>(launches) * r);
+        LAYA_HIP(hipStreamSynchronize(E->stream));
+        for (size_t i = 0; i < pairs; ++i) {
+          float ms = 0.f;
+          LAYA_HIP(hipEventElapsedTime(&ms, marks[2 * i], marks[2 * i + 1]));
+          total += ms;
         }
       } catch (...) {
         for (hipEvent_t e : marks)
