@@ -80,7 +80,10 @@ __device__ __forceinline__ void lds_load16(const void* g, unsigned lds) {
 // The same direct load through a buffer resource (buffer_load_dwordx4 ... offen lds): lane l fetches
 // 16 bytes at resource base + voffset(l) + soffset and the hardware writes them to LDS byte address
 // lds + 16 l (lds wave-uniform, in M0).  Loads past the resource's byte range return zeros.
+// soffset must be wave-uniform; readfirstlane puts it in an SGPR where the compiler computed it with
+// vector instructions (integer division of uniform values), and folds away where it already is one.
 __device__ __forceinline__ void lds_load16_buffer(i32x4 rsrc, unsigned voffset, unsigned soffset, unsigned lds) {
+  soffset = __builtin_amdgcn_readfirstlane(soffset);
   asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voffset), "s"(rsrc), "s"(soffset),
                "{m0}"(lds));
 }

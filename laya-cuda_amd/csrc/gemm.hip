@@ -30,6 +30,7 @@
 //   QKV_ROPE - QKV with rotate-half RoPE applied to Q and K in fp32 before the rounding.
 #include "kernels.hpp"
 
+#include <atomic>
 #include <type_traits>
 
 namespace laya {
@@ -53,15 +54,16 @@ __device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
 // operands.  Inside a slice, tiles are walked so the operand that is larger in HBM is fetched into
 // one L2 once: with many rows (A larger), groups of 4 tile rows with the column index outer; with
 // fewer rows than columns (B, the weights, larger), whole tile columns one after another.
-__device__ __forceinline__ void tile_coords(int nx, int ny, int nz, bool rows_major, int* x, int* y, int* z) {
+// Coordinates of logical tile `id` (0 .. nx ny nz - 1): the workgroup with linear dispatch id `id`
+// in the order above.
+__device__ __forceinline__ void tile_of(int id, int nx, int ny, int nz, bool rows_major, int* x, int* y, int* z) {
   const int per_z = nx * ny, total = per_z * nz;
   if (total % 8) {
-    *x = blockIdx.x;
-    *y = blockIdx.y;
-    *z = blockIdx.z;
+    *x = id % nx;
+    *y = (id / nx) % ny;
+    *z = id / per_z;
     return;
   }
-  const int id = blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z);
   const int l = (id % 8) * (total / 8) + id / 8;
   *z = l / per_z;
   const int t = l - *z * per_z;
@@ -74,6 +76,9 @@ __device__ __forceinline__ void tile_coords(int nx, int ny, int nz, bool rows_ma
     *x = t / ny;
     *y = t - *x * ny;
   }
+}
+__device__ __forceinline__ void tile_coords(int nx, int ny, int nz, bool rows_major, int* x, int* y, int* z) {
+  tile_of(blockIdx.x + nx * (blockIdx.y + ny * blockIdx.z), nx, ny, nz, rows_major, x, y, z);
 }
 
 // Bytes of LDS the epilogue stages through: one 32 x 36 fp32 (or 32 x 40 16-bit) region per wave.
@@ -104,8 +109,15 @@ __device__ __forceinline__ int quad_col(int lane, int r4) {
   return L16 ? ((r4 & 1) << 4) + ((lane >> 4) << 2) : 8 * r4 + 4 * (lane >> 5);
 }
 
-template <typename T, int BM, int BN, int WM, int WN, Epi E, bool kEarlyBias, bool L16 = false>
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[BM / WM / 32][BN / WN / 32],
+// Column quad r4 of a 32x32 accumulator region: held as one 16-register tile, or (persistent ring
+// with 16x16x32 MFMAs) as four 4-register quads.
+__device__ __forceinline__ f32x4 acc_quad(const f32x16& v, int r4) {
+  return f32x4{v[4 * r4], v[4 * r4 + 1], v[4 * r4 + 2], v[4 * r4 + 3]};
+}
+__device__ __forceinline__ f32x4 acc_quad(const f32x4 (&v)[4], int r4) { return v[r4]; }
+
+template <typename T, int BM, int BN, int WM, int WN, Epi E, bool kEarlyBias, bool L16 = false, typename Acc>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, Acc (&acc)[BM / WM / 32][BN / WN / 32],
                                               const float4 (&early_bias)[kEarlyBias ? BN / WN / 32 : 1][4],
                                               const int (&early_pos)[BM / WM / 32], int m0, int n0, int z,
                                               unsigned char* smem_raw, int lane, int wave) {
@@ -119,10 +131,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, f32x16 (&acc)[B
   // r%4 of output row l%32: a lane holds columns c..c+3 of one row for each r/4.  The bias joins in
   // fp32 before the single rounding.
   auto take = [&](int i, int j, int r4, float (&v)[4]) {
-    v[0] = acc[i][j][4 * r4];
-    v[1] = acc[i][j][4 * r4 + 1];
-    v[2] = acc[i][j][4 * r4 + 2];
-    v[3] = acc[i][j][4 * r4 + 3];
+    const f32x4 q = acc_quad(acc[i][j], r4);
+    v[0] = q[0];
+    v[1] = q[1];
+    v[2] = q[2];
+    v[3] = q[3];
     if (with_bias) {
       const float4 b = kEarlyBias ? early_bias[kEarlyBias ? j : 0][r4]
                                   : *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + j * 32 + quad_col<L16>(lane, r4));
@@ -819,12 +832,238 @@ void gemm_pipe_kernel(GemmArgs a) {
                                                        wave);
 }
 
+// Persistent form of the eight-wave 256x256 ring (tile 26: tile 19 looping over tiles).  A launch
+// of tile 19 runs in rounds of one 160 KB workgroup per CU, and every workgroup of a round fills its
+// pipeline, and later writes its 128 KB of output, at the same moment, with no other workgroup's
+// MFMAs to cover either.  Here a grid of at most one workgroup per CU walks the tiles id, id + G,
+// id + 2G, ... (G workgroups; the same XCD-aware order as a launch of all tiles, since workgroup id
+// and id + G run on the same XCD when G is a multiple of 8), and the ring's operand stream runs on
+// across tile boundaries: the loads issued during a tile's last two slabs fetch the next tile's
+// first slabs, so the next tile's MFMAs start as soon as the epilogue is done.  The epilogue stages
+// its rows in the ring buffer of the last slab's A half - free once the barrier after that slab's
+// LDS reads has passed, and no load is in flight into it - and the two loads the ring would issue
+// into that slab's buffers are issued after the epilogue instead.  Each tile's bias is loaded at the
+// tile's start, before any load of the next tile's slabs: vector memory operations complete in
+// issue order, so a bias load issued in the epilogue would wait for the whole prefetch (measured:
+// 5.5% of the up projection's time).  16-bit outputs without RoPE only (the fp32 epilogue's staging,
+// 37 KB, needs more than one 32 KB buffer); every tile's K range must hold at least three slabs
+// (the ring prefetches two slabs and an A half).
+template <typename T, Epi E>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_ring_persist_kernel(GemmArgs a) {
+  constexpr int BM = 256, BN = 256, WM = 2, WN = 4, NW = WM * WN, BKS = 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+  constexpr int CPR = BKS / 8, RPI = 64 / CPR, KS = BKS / 16;
+  constexpr int AG = BM / RPI / NW, BG = BN / RPI / NW, NLD = AG + BG;
+  constexpr int HALFE = BM * BKS;  // 16-bit elements of a ring buffer
+  static_assert(E != Epi::F32, "16-bit epilogues: their staging fits one ring buffer");
+  static_assert(NW * 32 * 40 * 2 <= HALFE * 2, "16-bit epilogue staging within one ring buffer");
+  static_assert(E != Epi::QKV_ROPE, "no RoPE (its cos/sin registers do not fit beside the tile loop's)");
+  constexpr int kWaitSlab = waitcnt_vm(AG);
+  constexpr int kWaitFirst = waitcnt_vm(2 * AG + BG);
+  constexpr int kWaitAll = waitcnt_vm(0);
+  typedef typename Vec8<T>::type T8;
+
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* const lds = reinterpret_cast<T*>(smem_raw);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+  const int lrow = lane & 31, kg = lane >> 5;
+
+  const int nx = a.N / BN, ny = (a.M + BM - 1) / BM, nz = a.splits, total = nx * ny * nz;
+  const int G = gridDim.x;
+  const int n = a.K / BKS / a.splits;  // slabs per tile (the launcher checks K / 64 % splits == 0, n >= 3)
+  int id = blockIdx.x;
+  if (id >= total) return;
+
+  // Operands through per-tile buffer resources based at the tile's first A row and first B row:
+  // a lane's byte offset in a tile's rows is the same for every tile (one register per load
+  // instruction), and A rows past M fall outside the A resource's range (M - m0 rows), which
+  // suppresses those loads; they feed only output rows past M, which are never stored.
+  const int lr = lane / CPR, pch = lane % CPR;
+  auto src_of = [&](int q) {
+    const int row = (wave + NW * (q < AG ? q : q - AG)) * RPI + lr;
+    return static_cast<unsigned>((row * (q < AG ? a.lda : a.ldb) + ((pch ^ swz_k<BKS>(row)) << 3)) * 2);
+  };
+  auto dst_of = [&](int q) { return (wave + NW * (q < AG ? q : q - AG)) * RPI * BKS; };
+  auto res_a = [&](int m0) {
+    return buffer_resource(static_cast<const T*>(a.a) + static_cast<size_t>(m0) * a.lda,
+                           static_cast<unsigned>(static_cast<size_t>(a.M - m0) * a.lda * 2));
+  };
+  auto res_b = [&](int n0) {
+    return buffer_resource(static_cast<const T*>(a.b) + static_cast<size_t>(n0) * a.ldb,
+                           static_cast<unsigned>(static_cast<size_t>(a.N - n0) * a.ldb * 2));
+  };
+  auto decode = [&](int t, int& m0, int& n0, int& z) {
+    int tx, ty;
+    tile_of(t, nx, ny, nz, a.rows_major, &tx, &ty, &z);
+    n0 = tx * BN;
+    m0 = ty * BM;
+  };
+  const unsigned lds_base = lds_address(smem_raw);
+
+  int m0, n0, z;
+  decode(id, m0, n0, z);
+  int kb = z * n;
+  i32x4 rsA = res_a(m0), rsB = res_b(n0);
+  int nid = id + G, nm0 = m0, nn0 = n0, nzz = z;
+  bool has_next = nid < total;
+  if (has_next) decode(nid, nm0, nn0, nzz);
+  i32x4 nrsA = res_a(nm0), nrsB = res_b(nn0);
+  int nkb = nzz * n;
+
+  // One half (A rows: q < AG, or B rows) of stream slab `s` counted from this tile's first slab:
+  // this tile's slab s, the next tile's slab s - n, or (last tile) this tile's last slab again,
+  // landing in a buffer that is never read.
+  auto issue_half = [&](bool isB, int s, int buf) {
+    const bool next = s >= n && has_next;
+    const int kt = next ? nkb + (s - n) : kb + min(s, n - 1);
+    const i32x4 r = isB ? (next ? nrsB : rsB) : (next ? nrsA : rsA);
+#pragma unroll
+    for (int q = isB ? AG : 0; q < (isB ? NLD : AG); ++q)
+      lds_load16_buffer(r, src_of(q), static_cast<unsigned>(kt) * BKS * 2,
+                        lds_base + static_cast<unsigned>(buf * HALFE + dst_of(q)) * 2);
+  };
+
+  // The tile's bias for this lane's column quads (as the small tiles' early bias), and the RoPE-free
+  // positions placeholder the epilogue takes.
+  float4 bias[TN][4];
+  auto load_bias = [&]() {
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        bias[j][r4] = a.bias ? *reinterpret_cast<const float4*>(a.bias + n0 + wn0 + j * 32 + quad_col<false>(lane, r4))
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  int early_pos[TM] = {};
+  load_bias();
+
+  f32x16 acc[TM][TN];
+  T8 af[2][TM], bfr[2][TN];
+  auto fetch = [&](int abuf, int bbuf, int kk, int s) {
+    const T* cA = lds + abuf * HALFE;
+    const T* cB = lds + bbuf * HALFE;
+    const int ch = kk * 2 + kg;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm0 + i * 32 + lrow;
+      af[s][i] = *reinterpret_cast<const T8*>(cA + r * BKS + ((ch ^ swz_k<BKS>(r)) << 3));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int r = wn0 + j * 32 + lrow;
+      bfr[s][j] = *reinterpret_cast<const T8*>(cB + r * BKS + ((ch ^ swz_k<BKS>(r)) << 3));
+    }
+  };
+  auto mma = [&](int s) {  // weights as the MFMA A operand: the accumulator holds C^T
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = mfma32(bfr[s][j], af[s][i], acc[i][j]);
+  };
+  auto hint = [&]() {  // LDS reads first, two per MFMA slot (as gemm_pipe_kernel's ring)
+    constexpr int NMF = TM * TN, NDS = TM + TN;
+#pragma unroll
+    for (int t = 0; t < NMF; ++t) {
+      if (2 * t < NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (2 * t + 1 < NDS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+  };
+  // The k-steps of a slab before its barrier: fragments of step kk+1 read during the MFMAs of kk.
+  auto slab_front = [&](int abuf, int bbuf) {
+#pragma unroll
+    for (int kk = 0; kk < KS - 1; ++kk) {
+      fetch(abuf, bbuf, kk + 1, (kk + 1) & 1);
+      mma(kk & 1);
+      hint();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Prologue: halves 0 .. 4 of the stream (slabs 0 and 1, A of slab 2) into buffers 0 .. 4.
+#pragma unroll
+  for (int h = 0; h < 5; ++h) issue_half(h & 1, h / 2, h);
+  publish_stage<kWaitFirst>();
+  fetch(0, 1, 0, 0);
+  int abuf = 0;  // buffer of the current slab's A half; its B half is in the next one
+  for (;;) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    for (int it = 0; it < n - 1; ++it) {
+      const int bbuf = abuf == 4 ? 0 : abuf + 1;
+      const int nabuf = abuf >= 3 ? abuf - 3 : abuf + 2, nbbuf = nabuf == 4 ? 0 : nabuf + 1;
+      slab_front(abuf, bbuf);
+      publish_stage<kWaitSlab>();
+      __builtin_amdgcn_sched_barrier(0);
+      fetch(nabuf, nbbuf, 0, 0);
+      issue_half(true, it + 2, abuf);   // B half of slab it+2 into the freed A buffer
+      issue_half(false, it + 3, bbuf);  // A half of slab it+3 into the freed B buffer
+      mma((KS - 1) & 1);
+      hint();
+      __builtin_amdgcn_sched_barrier(0);
+      abuf = nabuf;
+    }
+    // The tile's last slab.
+    const int bbuf = abuf == 4 ? 0 : abuf + 1;
+    const int nabuf = abuf >= 3 ? abuf - 3 : abuf + 2, nbbuf = nabuf == 4 ? 0 : nabuf + 1;
+    slab_front(abuf, bbuf);
+    publish_stage<kWaitSlab>();
+    __builtin_amdgcn_sched_barrier(0);
+    mma((KS - 1) & 1);
+    if (!has_next) {
+      // The clamped loads of the last slabs may still be landing: drain them before the epilogue
+      // reuses LDS (and before the workgroup ends).
+      __builtin_amdgcn_s_waitcnt(kWaitAll);
+      __syncthreads();
+      gemm_epilogue<T, BM, BN, WM, WN, E, true>(a, acc, bias, early_pos, m0, n0, z, smem_raw, lane, wave);
+      return;
+    }
+    gemm_epilogue<T, BM, BN, WM, WN, E, true>(a, acc, bias, early_pos, m0, n0, z,
+                                              smem_raw + static_cast<size_t>(abuf) * HALFE * 2, lane, wave);
+    // Every wave's staging reads are done before the ring loads below overwrite the buffer (the
+    // epilogue's global stores stay in flight).
+    __builtin_amdgcn_s_waitcnt(waitcnt_lgkm0_keep_vm());
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // Next tile: it becomes the current one, and the one after it the next.
+    id = nid;
+    m0 = nm0;
+    n0 = nn0;
+    z = nzz;
+    kb = nkb;
+    rsA = nrsA;
+    rsB = nrsB;
+    nid = id + G;
+    has_next = nid < total;
+    if (has_next) {
+      decode(nid, nm0, nn0, nzz);
+      nrsA = res_a(nm0);
+      nrsB = res_b(nn0);
+      nkb = nzz * n;
+    }
+    load_bias();
+    // The two loads the last slab's iteration deferred: B of the tile's slab 1, A of its slab 2.
+    issue_half(true, 1, abuf);
+    issue_half(false, 2, bbuf);
+    fetch(nabuf, nbbuf, 0, 0);
+    abuf = nabuf;
+  }
+}
+
 struct TileDef {
   int bm, bn, wm, wn;
   int pf;      // >= 2: register-staged kernel with pf slabs in flight; 0: pipelined direct-to-LDS kernel
   int bk, st;  // pipelined kernel: slab depth and LDS stages (ring: five half-slab buffers)
   bool ring;
   bool m16 = false;  // ring with 16x16x32 MFMAs (row-major and head-major epilogues without RoPE)
+  bool persist = false;  // ring looping over tiles, one workgroup per CU (16-bit epilogues)
   int threads() const { return 64 * wm * wn; }
 };
 // Tile menu; the planner picks per problem.  Ids are part of the op-level ABI (tests sweep them).
@@ -868,6 +1107,9 @@ constexpr TileDef kTiles[] = {
     {128, 64, 4, 2, 0, 64, 6},   // 23: 8 waves of 32x32
     {64, 128, 2, 4, 0, 64, 6},   // 24: 8 waves of 32x32
     {128, 128, 4, 2, 0, 64, 4},  // 25: 8 waves of 32x64
+    // Persistent form of tile 19 (gemm_ring_persist_kernel): a workgroup per CU walks the tiles, its
+    // operand stream running on from one tile into the next.
+    {256, 256, 2, 4, 0, 64, 5, true, false, true},  // 26
 };
 constexpr int kTileCount = sizeof(kTiles) / sizeof(kTiles[0]);
 
@@ -875,6 +1117,17 @@ constexpr size_t lds_bytes(const TileDef& d) {
   return d.pf     ? static_cast<size_t>(2) * (d.bm + d.bn) * BK * 2
          : d.ring ? static_cast<size_t>(5) * d.bm * d.bk * 2
                   : static_cast<size_t>(d.st) * (d.bm + d.bn) * d.bk * 2;
+}
+
+// Compute units of the current device (the persistent tiles' grid), queried once per device.
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v <= 0 && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+    cache[dev].store(v, std::memory_order_relaxed);
+  return v;
 }
 
 template <typename T, Epi E>
@@ -918,6 +1171,17 @@ hipError_t launch_t(const GemmArgs& a, int tile, hipStream_t stream) {
     LAYA_PIPE(23, 128, 64, 4, 2, 64, 6)
     LAYA_PIPE(24, 64, 128, 2, 4, 64, 6)
     LAYA_PIPE(25, 128, 128, 4, 2, 64, 4)
+    case 26: {
+      if constexpr (E == Epi::F32 || E == Epi::QKV_ROPE) {
+        return hipErrorInvalidValue;
+      } else {
+        const int cus = device_cus();
+        if (cus <= 0) return hipErrorInvalidDevice;
+        const dim3 pgrid(min(static_cast<long long>(grid.x) * grid.y * grid.z, static_cast<long long>(cus)));
+        LAYA_LAUNCH((gemm_ring_persist_kernel<T, E>), pgrid, block, lds, stream, a);
+      }
+      break;
+    }
 #undef LAYA_RING
 #undef LAYA_TILE
 #undef LAYA_PIPE
@@ -956,6 +1220,9 @@ hipError_t set_lds_attr() {
   LAYA_ATTR(23, gemm_pipe_kernel<T, 128, 64, 4, 2, 64, 6, E, false>)
   LAYA_ATTR(24, gemm_pipe_kernel<T, 64, 128, 2, 4, 64, 6, E, false>)
   LAYA_ATTR(25, gemm_pipe_kernel<T, 128, 128, 4, 2, 64, 4, E, false>)
+  if constexpr (E != Epi::F32 && E != Epi::QKV_ROPE) {
+    LAYA_ATTR(26, gemm_ring_persist_kernel<T, E>)
+  }
 #undef LAYA_ATTR
   return e;
 }
@@ -1041,6 +1308,13 @@ void gemm_plan(int M, int N, int K, Epi epi, DType t, int cus, int* tile, int* s
     if (best_cost >= 0) {
       // The ring with 16x16x32 MFMAs for the row-major epilogues: out/down 2-6%, up 5% faster on
       // 64K rows; the head-major QKV epilogue measured 4% slower with it, so QKV keeps tile 19.
+      // Both give way to the persistent ring (tile 26) when some CUs get more than one tile and a
+      // tile's K loop is at most 32 slabs: measured against the better of 19 and 22, 2-7% faster on
+      // the 64K-row QKV, up and out projections and 5-8% on the 15,360-row QKV and up projections,
+      // but 3-5% slower on the 64-slab down projection (four tiles per CU).
+      const long long tiles = static_cast<long long>((M + 255) / 256) * (N / 256);
+      const bool persist_ok = epi != Epi::F32 && !rope && tiles > cus && K / BK >= 3 && K / BK <= 32;
+      if (best == 19 && persist_ok) best = 26;
       if (best == 19 && (epi == Epi::F32 || epi == Epi::HALF || epi == Epi::GELU || epi == Epi::RELU)) best = 22;
       *tile = best;
       *splits = 1;
@@ -1085,6 +1359,9 @@ hipError_t launch_gemm(const GemmArgs& args, Epi epi, DType t, int tile, hipStre
   // RoPE needs both halves of a head in one lane: wave tiles of 64-column multiples.
   const TileDef& td = kTiles[tile];
   if (td.m16 && (epi == Epi::QKV_ROPE || epi == Epi::GEGLU)) return hipErrorInvalidValue;
+  // Persistent tiles: 16-bit outputs without RoPE, at least three 64-deep slabs per tile.
+  if (td.persist && (epi == Epi::F32 || epi == Epi::QKV_ROPE || (a.K / BK) % a.splits || a.K / BK / a.splits < 3))
+    return hipErrorInvalidValue;
   if (epi == Epi::QKV_ROPE && (td.bn / td.wn) % 64) return hipErrorInvalidValue;
   if ((epi == Epi::QKV || epi == Epi::QKV_ROPE) && a.M % 8) return hipErrorInvalidValue;  // V^T: runs of 8 tokens
   if (epi == Epi::GEGLU && (a.N % 32 || a.ldo * 2 < a.N)) return hipErrorInvalidValue;

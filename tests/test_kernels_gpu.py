@@ -240,8 +240,9 @@ def linear(x, w, bias, out, kind, dtype, M, N, K, splits, tile):
     sync()
 
 
-GEMM_TILES = 26  # tile ids of laya_op_linear (csrc/gemm.hip kTiles)
+GEMM_TILES = 27  # tile ids of laya_op_linear (csrc/gemm.hip kTiles)
 TILE_BN = {21: 192}  # tiles whose width is not a power of two
+PERSISTENT = {26}  # tiles looping over output tiles: 16-bit epilogues without RoPE only
 
 
 def ncols(N, tile):
@@ -251,7 +252,7 @@ def ncols(N, tile):
 
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
-@pytest.mark.parametrize("tile", range(GEMM_TILES))
+@pytest.mark.parametrize("tile", [t for t in range(GEMM_TILES) if t not in PERSISTENT])
 def test_linear_tiles_match_fp32_product(gpu, dtype, tile):
     t = torch()
     rng = np.random.default_rng(tile)
@@ -296,6 +297,84 @@ def test_linear_split_k_partials_sum_to_the_product(gpu, splits, tile):
     linear(to16(x, "f16", gpu), to16(w, "f16", gpu), None, out, 0, "f16", M, N, K, splits, tile)
     np.testing.assert_allclose(out.sum(0).cpu().numpy(), x.astype(np.float64) @ w.T.astype(np.float64),
                                atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("kind", [1, 2, 3, 4])
+@pytest.mark.parametrize("M,N,K", [(16421, 2048, 192), (30000, 768, 320), (8192, 8192, 1024)])
+def test_persistent_tile_walks_many_tiles_per_workgroup(gpu, kind, M, N, K):
+    """Tile 26 runs at most one workgroup per CU, each walking several 256x256 output tiles with
+    the next tile's first slabs loaded during the current tile's last ones.  On 256 CUs: 520 tiles
+    (two or three per workgroup) with a partial last row tile and the three-slab minimum, 354
+    tiles (a count that is not a multiple of 8, so the plain tile order), and 1,024 tiles (four
+    per workgroup).  Reference: torch fp32 on the same 16-bit operands."""
+    t = torch()
+    g = t.Generator(device=gpu).manual_seed(M + K + kind)
+    x = t.randn((M, K), generator=g, device=gpu).half()
+    w = (t.randn((N, K), generator=g, device=gpu) / math.sqrt(K)).half()
+    bias = t.randn(N, generator=g, device=gpu) * 0.5
+    ref = t.addmm(bias, x.float(), w.float().t())
+    if kind == 2:
+        ref = t.nn.functional.gelu(ref)
+    elif kind == 3:
+        ref = t.relu(ref)
+    elif kind == 4:  # GeGLU over the 32-row interleave: 16 gate rows, then their 16 value rows
+        groups = ref.view(M, N // 32, 2, 16)
+        ref = (t.nn.functional.gelu(groups[:, :, 0]) * groups[:, :, 1]).reshape(M, N // 2)
+    out = t.full((M, N // 2 if kind == 4 else N), float("nan"), dtype=t.float16, device=gpu)
+    lib = _lib.load()
+    check(lib.laya_op_linear(p(x), p(w), None if kind == 4 else p(bias), p(out), kind, _lib.F16, M, N, K, 1, 26,
+                             stream()))
+    sync()
+    if kind == 4:  # the GeGLU epilogue takes no bias: compare against the product without it
+        groups = t.mm(x.float(), w.float().t()).view(M, N // 32, 2, 16)
+        ref = (t.nn.functional.gelu(groups[:, :, 0]) * groups[:, :, 1]).reshape(M, N // 2)
+    got = out.float()
+    assert t.isfinite(got).all()
+    err = (got - ref).abs().max().item()
+    assert err <= 2e-3 * max(1.0, ref.abs().max().item()), err
+
+
+def test_persistent_qkv_walks_many_tiles_per_workgroup(gpu):
+    """The head-major QKV epilogue on tile 26 with several tiles per workgroup: integer-valued
+    operands make the product exact, so the layout check is bit-exact."""
+    t = torch()
+    rng = np.random.default_rng(26)
+    M, heads = 8200, 16  # 33 row tiles x 12 column tiles = 396 tiles
+    width = heads * 64
+    x = rng.integers(-3, 4, (M, width)).astype(np.float32)
+    w = rng.integers(-2, 3, (3 * width, width)).astype(np.float32)
+    bias = rng.integers(-4, 5, 3 * width).astype(np.float32)
+    q, k, vt = (t.full((heads * M * 64,), float("nan"), dtype=t.float16, device=gpu) for _ in range(3))
+    d_x, d_w, d_bias = to16(x, "f16", gpu), to16(w, "f16", gpu), dev(bias, gpu)
+    check(_lib.load().laya_op_qkv(p(d_x), p(d_w), p(d_bias), p(q), p(k), p(vt), None, None, None, _lib.F16, M, width,
+                                  26, stream()))
+    sync()
+    full = x @ w.T + bias
+    parts = full.reshape(M, 3, heads, 64)
+    np.testing.assert_array_equal(q.cpu().numpy().reshape(heads, M, 64), parts[:, 0].transpose(1, 0, 2))
+    np.testing.assert_array_equal(k.cpu().numpy().reshape(heads, M, 64), parts[:, 1].transpose(1, 0, 2))
+    np.testing.assert_array_equal(vt.cpu().numpy().reshape(heads, 64, M), parts[:, 2].transpose(1, 2, 0))
+
+
+def test_persistent_tile_refuses_fp32_rope_and_short_k(gpu):
+    """Tile 26 stages its epilogue in one 32 KB ring buffer (16-bit outputs only), has no RoPE form
+    and needs three 64-deep slabs per tile: those launches return an error instead of running."""
+    t = torch()
+    M, width = 512, 256
+    x = t.zeros((M, 1024), dtype=t.float16, device=gpu)
+    w = t.zeros((3 * width, 1024), dtype=t.float16, device=gpu)
+    out32 = t.zeros((M, width), device=gpu)
+    out16 = t.zeros((M, width), dtype=t.float16, device=gpu)
+    lib = _lib.load()
+    assert lib.laya_op_linear(p(x), p(w), None, p(out32), 0, _lib.F16, M, width, 1024, 1, 26, stream()) != 0
+    assert lib.laya_op_linear(p(x), p(w), None, p(out16), 1, _lib.F16, M, width, 128, 1, 26, stream()) != 0
+    assert lib.laya_op_linear(p(x), p(w), None, p(out16), 1, _lib.F16, M, width, 192, 1, 26, stream()) == 0
+    q, k, vt = (t.zeros((M * width,), dtype=t.float16, device=gpu) for _ in range(3))
+    cos, sin = t.ones((M, 32), device=gpu), t.zeros((M, 32), device=gpu)
+    pos = t.zeros(M, dtype=t.int32, device=gpu)
+    assert lib.laya_op_qkv(p(x), p(w), None, p(q), p(k), p(vt), p(cos), p(sin), p(pos), _lib.F16, M, width, 26,
+                           stream()) != 0
+    sync()
 
 
 def test_linear_adds_bias_before_rounding(gpu):
@@ -350,7 +429,7 @@ def test_sixteen_wide_mfma_tile_refuses_rope_and_geglu(gpu):
     sync()
 
 
-@pytest.mark.parametrize("tile", [0, 2, 5, 6, 7, 9, 11, 12, 13, 14, 16, 18, 19, 20, 21, 22])
+@pytest.mark.parametrize("tile", [0, 2, 5, 6, 7, 9, 11, 12, 13, 14, 16, 18, 19, 20, 21, 22, 26])
 def test_qkv_epilogue_writes_head_major_layout(gpu, tile):
     """Integer-valued operands make the product exact, so the layout check is bit-exact."""
     t = torch()
