@@ -109,12 +109,10 @@ __device__ __forceinline__ int quad_col(int lane, int r4) {
   return L16 ? ((r4 & 1) << 4) + ((lane >> 4) << 2) : 8 * r4 + 4 * (lane >> 5);
 }
 
-// Column quad r4 of a 32x32 accumulator region: held as one 16-register tile, or (persistent ring
-// with 16x16x32 MFMAs) as four 4-register quads.
+// Column quad r4 of a 32x32 accumulator region (one 16-register tile).
 __device__ __forceinline__ f32x4 acc_quad(const f32x16& v, int r4) {
   return f32x4{v[4 * r4], v[4 * r4 + 1], v[4 * r4 + 2], v[4 * r4 + 3]};
 }
-__device__ __forceinline__ f32x4 acc_quad(const f32x4 (&v)[4], int r4) { return v[r4]; }
 
 template <typename T, int BM, int BN, int WM, int WN, Epi E, bool kEarlyBias, bool L16 = false, typename Acc>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, Acc (&acc)[BM / WM / 32][BN / WN / 32],
