@@ -1245,6 +1245,8 @@ GemmTile gemm_tile(int id) { return GemmTile{kTiles[id].bm, kTiles[id].bn}; }
 hipError_t gemm_prepare() {
   hipError_t e = set_lds_all<bf16>();
   if (e == hipSuccess) e = set_lds_all<f16>();
+  // The persistent tile's grid reads the CU count at launch: query it here, before any capture.
+  if (e == hipSuccess && device_cus() <= 0) e = hipErrorInvalidDevice;
   return e;
 }
 
