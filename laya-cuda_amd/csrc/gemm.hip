@@ -880,9 +880,10 @@ void gemm_ring_persist_kernel(GemmArgs a) {
   // instruction), and A rows past M fall outside the A resource's range (M - m0 rows), which
   // suppresses those loads; they feed only output rows past M, which are never stored.
   const int lr = lane / CPR, pch = lane % CPR;
-  auto src_of = [&](int q) {
+  auto src_of = [&](int q) {  // unsigned: 32-bit offsets (the launcher bounds each operand below 4 GiB)
     const int row = (wave + NW * (q < AG ? q : q - AG)) * RPI + lr;
-    return static_cast<unsigned>((row * (q < AG ? a.lda : a.ldb) + ((pch ^ swz_k<BKS>(row)) << 3)) * 2);
+    const unsigned ld = static_cast<unsigned>(q < AG ? a.lda : a.ldb);
+    return (static_cast<unsigned>(row) * ld + (static_cast<unsigned>(pch ^ swz_k<BKS>(row)) << 3)) * 2u;
   };
   auto dst_of = [&](int q) { return (wave + NW * (q < AG ? q : q - AG)) * RPI * BKS; };
   auto res_a = [&](int m0) {
