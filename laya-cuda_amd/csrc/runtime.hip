@@ -120,8 +120,11 @@ struct Slot {
   size_t bytes = 0;
   int32_t* d_packed = nullptr;
   int32_t* h_packed = nullptr;
+  // Pinned host copy of the device logits and acts, which the arena keeps next to each other: one
+  // D2H copy brings both (h_acts points into the same allocation, at the device layout's offset).
   float* h_logits = nullptr;
   float* h_acts = nullptr;
+  size_t h_out_bytes = 0;
   float* residual = nullptr;
   void *x = nullptr, *q = nullptr, *kk = nullptr, *vt = nullptr, *attn = nullptr, *ff = nullptr;
   float* part = nullptr;
@@ -300,7 +303,6 @@ void destroy_slot(Engine& E, Slot* s) {
   if (s->arena) (void)hipFree(s->arena);
   if (s->h_packed) (void)hipHostFree(s->h_packed);
   if (s->h_logits) (void)hipHostFree(s->h_logits);
-  if (s->h_acts) (void)hipHostFree(s->h_acts);
   E.slot_bytes -= s->bytes;
   delete s;
 }
@@ -723,8 +725,10 @@ Slot* create_slot(Engine& E, int m, int b, int k) {
     E.slot_bytes += total;
     carve_slot(E, s, static_cast<char*>(s->arena));
     LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_packed), s->L.total * 4, hipHostMallocDefault));
-    LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_logits), static_cast<size_t>(b) * (k + 1) * 4, hipHostMallocDefault));
-    LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_acts), static_cast<size_t>(b) * E.cfg.n_act * 4, hipHostMallocDefault));
+    const size_t acts_at = reinterpret_cast<char*>(s->acts) - reinterpret_cast<char*>(s->logits);
+    s->h_out_bytes = acts_at + static_cast<size_t>(b) * E.cfg.n_act * 4;
+    LAYA_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_logits), s->h_out_bytes, hipHostMallocDefault));
+    s->h_acts = reinterpret_cast<float*>(reinterpret_cast<char*>(s->h_logits) + acts_at);
     LAYA_HIP(hipEventCreate(&s->start));
     LAYA_HIP(hipEventCreate(&s->end));
   } catch (...) {
@@ -1127,8 +1131,7 @@ int laya_predict(void* handle, const int32_t* host_packed, const LayaShape* shap
       forward(*E, *s);
     }
     LAYA_HIP(hipEventRecord(s->end, E->stream));
-    LAYA_HIP(hipMemcpyAsync(s->h_logits, s->logits, static_cast<size_t>(b) * (k + 1) * 4, hipMemcpyDeviceToHost, E->stream));
-    LAYA_HIP(hipMemcpyAsync(s->h_acts, s->acts, static_cast<size_t>(b) * E->cfg.n_act * 4, hipMemcpyDeviceToHost, E->stream));
+    LAYA_HIP(hipMemcpyAsync(s->h_logits, s->logits, s->h_out_bytes, hipMemcpyDeviceToHost, E->stream));
     LAYA_HIP(hipStreamSynchronize(E->stream));
     float ms = 0.f;
     LAYA_HIP(hipEventElapsedTime(&ms, s->start, s->end));
